@@ -1,0 +1,90 @@
+"""ctypes binding of the C ABI in `include/attnres_hip.h`.
+
+The shared library `_lib/libattnres_hip.so` is built in-tree from
+`csrc/attnres_hip.hip` by `build_native.py` (hipcc, gfx950).  There is no
+fallback: if the library is missing or does not load, every operator call
+raises, so a GPU run can never silently take another path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIBRARY_NAME = "libattnres_hip.so"
+LIBRARY_PATH = Path(__file__).resolve().parent / "_lib" / LIBRARY_NAME
+
+# Status codes of `enum attnres_status`.
+OK = 0
+ERR_NULL_POINTER = 1
+ERR_SHAPE = 2
+ERR_STRIDE = 3
+ERR_SCALAR = 4
+ERR_WORKSPACE = 5
+ERR_LAUNCH = 6
+
+_c_void_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+
+# name -> (restype, argtypes); one entry per declaration in attnres_hip.h.
+SIGNATURES = {
+    "attnres_hip_version": (ctypes.c_char_p, []),
+    "attnres_hip_last_error": (ctypes.c_char_p, []),
+    "attnres_hip_dq_workspace_elems": (_i64, [_i64, _i64, _i64]),
+    "attnres_hip_packed_forward": (ctypes.c_int, [
+        _c_void_p, _i64, _i64, _i64, _i64, _i64, _c_void_p, _i64, _f32, _f32,
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p]),
+    "attnres_hip_packed_backward": (ctypes.c_int, [
+        _c_void_p, _i64, _i64, _i64, _i64, _i64, _c_void_p, _i64, _f32,
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+        _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p]),
+    "attnres_hip_sources_forward": (ctypes.c_int, [
+        _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _f32, _f32,
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p]),
+    "attnres_hip_sources_backward": (ctypes.c_int, [
+        _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _f32,
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+        _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p]),
+}
+
+_lock = threading.Lock()
+_library: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the native library, or raise RuntimeError."""
+    global _library
+    if _library is not None:
+        return _library
+    with _lock:
+        if _library is None:
+            path = LIBRARY_PATH
+            if not path.is_file():
+                raise RuntimeError(
+                    f"attnres HIP extension not built: {path} is missing "
+                    "(run `python fast-attnres_amd/build_native.py`)")
+            try:
+                library = ctypes.CDLL(str(path))
+            except OSError as error:
+                raise RuntimeError(f"attnres HIP extension failed to load: {error}") from error
+            for name, (restype, argtypes) in SIGNATURES.items():
+                function = getattr(library, name)
+                function.restype = restype
+                function.argtypes = argtypes
+            _library = library
+    return _library
+
+
+def check(status: int, what: str) -> None:
+    """Raise for a non-OK status, with the library's own message."""
+    if status == OK:
+        return
+    message = (load().attnres_hip_last_error() or b"").decode(errors="replace")
+    if status in (ERR_SHAPE, ERR_STRIDE, ERR_SCALAR, ERR_WORKSPACE):
+        raise ValueError(f"{what}: {message}")
+    raise RuntimeError(f"{what}: {message} (status {status})")
+
+
+__all__ = ["LIBRARY_PATH", "SIGNATURES", "check", "load"]

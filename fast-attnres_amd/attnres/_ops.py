@@ -1,0 +1,332 @@
+"""torch.library operators for the HIP read, their fake (meta) kernels and autograd.
+
+Four opaque ops in the ``attnres_hip`` namespace stand where the reference
+registers ``attnres::_fixed_tail_forward_with_aux`` / ``_fixed_tail_backward``
+(packed, `src/attnres/_kernels/fixed_tail.py:902-1094`) and
+``attnres::_fixed_tail_sources_forward_with_aux`` / ``_fixed_tail_sources_backward``
+(list, `src/attnres/_kernels/fixed_tail_sources.py:78-183`):
+
+* ``packed_forward(values[S,N,D], query[R], eps, scale)``
+  -> ``(out[N,D] bf16, out_refine[N,D] int8, logit[N,S] f32, inv_rms[N,S] f32,
+  stats[2,N] f32)``
+* ``packed_backward(values, query, out, out_refine, grad_out, logit, inv_rms,
+  stats, scale)`` -> ``(grad_values[S,N,D] bf16, grad_query[R] bf16)``
+* ``sources_forward(sources: list, query, eps, scale)`` -> same five tensors,
+  ``out`` shaped like one source
+* ``sources_backward(sources, query, out, out_refine, grad_out, logit, inv_rms,
+  stats, scale)`` -> ``[grad_source_0, ..., grad_source_{S-1}, grad_query]``
+
+Every output and workspace is allocated here with ``torch.empty`` on the
+caller's device; the kernels run on the current stream and the C ABI never
+allocates or synchronises, so the ops are safe under ``torch.compile``
+(opaque custom ops with fake kernels) and HIP/CUDA graph capture.
+
+Saved for backward: the inputs, the BF16 output plus one refinement byte
+per element (together the FP32 mix to ulp/512, for ``delta = <dO, o>``) and
+the small statistics.  The reference instead keeps an FP32 copy of the
+output (`fixed_tail.py:917-919`): four extra bytes per element written in
+the forward and read in the backward instead of one.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Any
+
+import torch
+from torch import Tensor
+
+from . import _native
+
+_F32 = torch.float32
+_BF16 = torch.bfloat16
+_OP_TAGS = (torch.Tag.flexible_layout,) if hasattr(torch.Tag, "flexible_layout") else ()
+
+
+# ------------------------------------------------------------------ layouts
+
+def row_stride(tensor: Tensor) -> int | None:
+    """Element stride between consecutive rows of ``tensor[..., D]`` flattened
+    to ``[rows, D]``, or None when the rows are not evenly spaced or a row is
+    not unit-stride.  Size-1 dimensions place no constraint; a single row
+    reports 0.  (Same flattening rule as the reference's
+    `fla_full_sources._affine_row_stride`, `fla_full_sources.py:164-178`, plus
+    the unit feature stride the 16-byte loads rely on.)"""
+    if tensor.shape[-1] > 1 and tensor.stride(-1) != 1:
+        return None
+    stride: int | None = None
+    rows = 1
+    for size, step in zip(reversed(tensor.shape[:-1]), reversed(tensor.stride()[:-1])):
+        if size == 1:
+            continue
+        if stride is None:
+            stride = int(step)
+        elif int(step) != rows * stride:
+            return None
+        rows *= int(size)
+    return 0 if stride is None else stride
+
+
+def prepare_rows(tensor: Tensor) -> tuple[Tensor, int]:
+    """The tensor itself when its rows are addressable, else a contiguous copy."""
+    stride = row_stride(tensor)
+    if stride is None:
+        tensor = tensor.contiguous()
+        stride = row_stride(tensor)
+        assert stride is not None
+    return tensor, stride
+
+
+def _unit_feature_stride(values: Tensor) -> Tensor:
+    if values.shape[-1] > 1 and values.stride(-1) != 1:
+        return values.contiguous()
+    return values
+
+
+def _contiguous(tensor: Tensor) -> Tensor:
+    return tensor if tensor.is_contiguous() else tensor.contiguous()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _rows_of(shape) -> int:
+    return math.prod(int(size) for size in shape[:-1]) if len(shape) > 1 else 1
+
+
+def _dq_workspace(lib, n_tokens: int, width: int, rank: int, device) -> Tensor:
+    elems = int(lib.attnres_hip_dq_workspace_elems(n_tokens, width, rank))
+    if elems < 0:
+        raise ValueError("attnres backward: shape outside the supported envelope")
+    return torch.empty((elems,), device=device, dtype=_F32)
+
+
+# ------------------------------------------------------------------ packed
+
+@torch.library.custom_op("attnres_hip::packed_forward", mutates_args=(),
+                         device_types="cuda", tags=_OP_TAGS)
+def packed_forward(values: Tensor, query: Tensor, eps: float,
+                   scale: float) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    lib = _native.load()
+    values = _unit_feature_stride(values)
+    query = _contiguous(query)
+    sources, tokens, width = (int(size) for size in values.shape)
+    device = values.device
+    out = torch.empty((tokens, width), device=device, dtype=_BF16)
+    out_refine = torch.empty((tokens, width), device=device, dtype=torch.int8)
+    logit = torch.empty((tokens, sources), device=device, dtype=_F32)
+    inv_rms = torch.empty((tokens, sources), device=device, dtype=_F32)
+    stats = torch.empty((2, tokens), device=device, dtype=_F32)
+    with torch.cuda.device(device):
+        status = lib.attnres_hip_packed_forward(
+            values.data_ptr(), values.stride(0), values.stride(1), sources, tokens, width,
+            query.data_ptr(), query.numel(), eps, scale, out.data_ptr(), out_refine.data_ptr(),
+            logit.data_ptr(), inv_rms.data_ptr(), stats.data_ptr(), _stream(device))
+    _native.check(status, "attnres packed forward")
+    return out, out_refine, logit, inv_rms, stats
+
+
+@packed_forward.register_fake
+def _packed_forward_fake(values, query, eps, scale):
+    sources, tokens, width = values.shape
+    return (values.new_empty((tokens, width)),
+            values.new_empty((tokens, width), dtype=torch.int8),
+            values.new_empty((tokens, sources), dtype=_F32),
+            values.new_empty((tokens, sources), dtype=_F32),
+            values.new_empty((2, tokens), dtype=_F32))
+
+
+@torch.library.custom_op("attnres_hip::packed_backward", mutates_args=(),
+                         device_types="cuda", tags=_OP_TAGS)
+def packed_backward(values: Tensor, query: Tensor, out: Tensor, out_refine: Tensor,
+                    grad_out: Tensor, logit: Tensor, inv_rms: Tensor, stats: Tensor,
+                    scale: float) -> tuple[Tensor, Tensor]:
+    lib = _native.load()
+    values = _unit_feature_stride(values)
+    query = _contiguous(query)
+    out = _contiguous(out)
+    grad_out = _contiguous(grad_out.to(_BF16))
+    sources, tokens, width = (int(size) for size in values.shape)
+    rank = query.numel()
+    device = values.device
+    grad_values = torch.empty((sources, tokens, width), device=device, dtype=_BF16)
+    grad_query = torch.empty((rank,), device=device, dtype=_BF16)
+    workspace = _dq_workspace(lib, tokens, width, rank, device)
+    with torch.cuda.device(device):
+        status = lib.attnres_hip_packed_backward(
+            values.data_ptr(), values.stride(0), values.stride(1), sources, tokens, width,
+            query.data_ptr(), rank, scale, out.data_ptr(), _contiguous(out_refine).data_ptr(),
+            grad_out.data_ptr(), _contiguous(logit).data_ptr(), _contiguous(inv_rms).data_ptr(),
+            _contiguous(stats).data_ptr(), grad_values.data_ptr(), grad_query.data_ptr(),
+            workspace.data_ptr(), workspace.numel(), _stream(device))
+    _native.check(status, "attnres packed backward")
+    return grad_values, grad_query
+
+
+@packed_backward.register_fake
+def _packed_backward_fake(values, query, out, out_refine, grad_out, logit, inv_rms, stats,
+                          scale):
+    return (values.new_empty(values.shape),
+            query.new_empty(query.shape))
+
+
+def _packed_setup_context(ctx: Any, inputs: tuple, output: tuple) -> None:
+    values, query, _eps, scale = inputs
+    out, out_refine, logit, inv_rms, stats = output
+    ctx.mark_non_differentiable(out_refine, logit, inv_rms, stats)
+    ctx.set_materialize_grads(False)
+    ctx.save_for_backward(values, query, out, out_refine, logit, inv_rms, stats)
+    ctx.scale = float(scale)
+
+
+def _packed_autograd(ctx: Any, grad_out, *_aux_grads):
+    if grad_out is None:
+        return None, None, None, None
+    values, query, out, out_refine, logit, inv_rms, stats = ctx.saved_tensors
+    grad_values, grad_query = packed_backward(
+        values, query, out, out_refine, grad_out, logit, inv_rms, stats, ctx.scale)
+    return (grad_values if ctx.needs_input_grad[0] else None,
+            grad_query if ctx.needs_input_grad[1] else None, None, None)
+
+
+packed_forward.register_autograd(_packed_autograd, setup_context=_packed_setup_context)
+
+
+def packed_attnres(values: Tensor, query: Tensor, eps: float, scale: float) -> Tensor:
+    """Packed ``[S, ..., D]`` adapter (reference `fixed_tail.fused_attnres`,
+    `fixed_tail.py:1097-1135`): flatten the batch axes to ``[S, N, D]`` as a
+    view when the layout allows it (a copy only otherwise), call the op and
+    restore the batch shape."""
+    sources, width = int(values.shape[0]), int(values.shape[-1])
+    flat = values.reshape(sources, -1, width)
+    if width > 1 and flat.stride(2) != 1:
+        flat = flat.contiguous()
+    out = packed_forward(flat, _contiguous(query), eps, scale)[0]
+    return out.reshape(values.shape[1:])
+
+
+# -------------------------------------------------------------------- list
+
+def _source_table(sources: list[Tensor]) -> tuple[list[Tensor], Any, Any]:
+    prepared, strides = [], []
+    for source in sources:
+        tensor, stride = prepare_rows(source)
+        prepared.append(tensor)
+        strides.append(stride)
+    count = len(prepared)
+    pointers = (ctypes.c_void_p * count)(*[tensor.data_ptr() for tensor in prepared])
+    row_strides = (ctypes.c_int64 * count)(*strides)
+    return prepared, pointers, row_strides
+
+
+@torch.library.custom_op("attnres_hip::sources_forward", mutates_args=(),
+                         device_types="cuda", tags=_OP_TAGS)
+def sources_forward(sources: list[Tensor], query: Tensor, eps: float,
+                    scale: float) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    lib = _native.load()
+    first = sources[0]
+    query = _contiguous(query)
+    count, tokens, width = len(sources), _rows_of(first.shape), int(first.shape[-1])
+    device = first.device
+    prepared, pointers, row_strides = _source_table(sources)
+    out = torch.empty(first.shape, device=device, dtype=_BF16)
+    out_refine = torch.empty((tokens, width), device=device, dtype=torch.int8)
+    logit = torch.empty((tokens, count), device=device, dtype=_F32)
+    inv_rms = torch.empty((tokens, count), device=device, dtype=_F32)
+    stats = torch.empty((2, tokens), device=device, dtype=_F32)
+    with torch.cuda.device(device):
+        status = lib.attnres_hip_sources_forward(
+            pointers, row_strides, count, tokens, width, query.data_ptr(), query.numel(),
+            eps, scale, out.data_ptr(), out_refine.data_ptr(), logit.data_ptr(),
+            inv_rms.data_ptr(), stats.data_ptr(), _stream(device))
+    del prepared  # copies (if any) stay alive until the launch is enqueued
+    _native.check(status, "attnres source-list forward")
+    return out, out_refine, logit, inv_rms, stats
+
+
+@sources_forward.register_fake
+def _sources_forward_fake(sources, query, eps, scale):
+    first = sources[0]
+    count, tokens = len(sources), _rows_of(first.shape)
+    return (first.new_empty(first.shape),
+            first.new_empty((tokens, int(first.shape[-1])), dtype=torch.int8),
+            first.new_empty((tokens, count), dtype=_F32),
+            first.new_empty((tokens, count), dtype=_F32),
+            first.new_empty((2, tokens), dtype=_F32))
+
+
+@torch.library.custom_op("attnres_hip::sources_backward", mutates_args=(),
+                         device_types="cuda", tags=_OP_TAGS)
+def sources_backward(sources: list[Tensor], query: Tensor, out: Tensor, out_refine: Tensor,
+                     grad_out: Tensor, logit: Tensor, inv_rms: Tensor, stats: Tensor,
+                     scale: float) -> list[Tensor]:
+    lib = _native.load()
+    first = sources[0]
+    query = _contiguous(query)
+    out = _contiguous(out)
+    grad_out = _contiguous(grad_out.to(_BF16))
+    count, tokens, width = len(sources), _rows_of(first.shape), int(first.shape[-1])
+    rank = query.numel()
+    device = first.device
+    prepared, pointers, row_strides = _source_table(sources)
+    grads = [torch.empty(first.shape, device=device, dtype=_BF16) for _ in range(count)]
+    grad_pointers = (ctypes.c_void_p * count)(*[grad.data_ptr() for grad in grads])
+    grad_query = torch.empty((rank,), device=device, dtype=_BF16)
+    workspace = _dq_workspace(lib, tokens, width, rank, device)
+    with torch.cuda.device(device):
+        status = lib.attnres_hip_sources_backward(
+            pointers, row_strides, count, tokens, width, query.data_ptr(), rank, scale,
+            out.data_ptr(), _contiguous(out_refine).data_ptr(), grad_out.data_ptr(),
+            _contiguous(logit).data_ptr(),
+            _contiguous(inv_rms).data_ptr(), _contiguous(stats).data_ptr(), grad_pointers,
+            grad_query.data_ptr(), workspace.data_ptr(), workspace.numel(), _stream(device))
+    del prepared
+    _native.check(status, "attnres source-list backward")
+    return [*grads, grad_query]
+
+
+@sources_backward.register_fake
+def _sources_backward_fake(sources, query, out, out_refine, grad_out, logit, inv_rms, stats,
+                           scale):
+    return [source.new_empty(source.shape)
+            for source in sources] + [query.new_empty(query.shape)]
+
+
+def _sources_setup_context(ctx: Any, inputs: tuple, output: tuple) -> None:
+    sources, query, _eps, scale = inputs
+    out, out_refine, logit, inv_rms, stats = output
+    ctx.mark_non_differentiable(out_refine, logit, inv_rms, stats)
+    ctx.set_materialize_grads(False)
+    ctx.save_for_backward(*sources, query, out, out_refine, logit, inv_rms, stats)
+    ctx.count = len(sources)
+    ctx.scale = float(scale)
+
+
+def _sources_autograd(ctx: Any, grad_out, *_aux_grads):
+    count = ctx.count
+    if grad_out is None:
+        return [None] * count, None, None, None
+    saved = ctx.saved_tensors
+    sources = list(saved[:count])
+    query, out, out_refine, logit, inv_rms, stats = saved[count:]
+    grads = sources_backward(sources, query, out, out_refine, grad_out, logit, inv_rms, stats,
+                             ctx.scale)
+    return list(grads[:count]), grads[count], None, None
+
+
+sources_forward.register_autograd(_sources_autograd, setup_context=_sources_setup_context)
+
+
+def sources_attnres(sources: tuple[Tensor, ...], query: Tensor, eps: float,
+                    scale: float) -> Tensor:
+    """Ordered source-list adapter (reference `fixed_tail_sources.source_attnres`,
+    `fixed_tail_sources.py:186-195`): the list is passed through unpacked."""
+    return sources_forward(list(sources), _contiguous(query), eps, scale)[0]
+
+
+__all__ = [
+    "packed_attnres", "packed_backward", "packed_forward", "prepare_rows", "row_stride",
+    "sources_attnres", "sources_backward", "sources_forward",
+]

@@ -1,0 +1,162 @@
+/*
+ * attnres_hip.h - C ABI of the MI355X (gfx950) Fast-AttnRes read.
+ *
+ * One AttnRes "read" mixes S depth sources of N token rows of width D with a
+ * static query q[R] (1 <= R <= D).  The key of source s at token n is the
+ * last R coordinates of its value row:
+ *
+ *   t_s = v_s[D-R:D];  r_s = sqrt(mean(t_s^2) + eps);  z_s = scale*<t_s/r_s, q>
+ *   p_s = softmax_s(z);  out = sum_s p_s * v_s
+ *
+ * Storage is BF16 (values, query, output, gradients); all arithmetic is FP32.
+ *
+ * Conventions shared by every entry point:
+ *   - every pointer is a device pointer unless stated otherwise; sizes and
+ *     strides are counted in ELEMENTS, not bytes;
+ *   - a value row is unit-stride along D; rows of one source are
+ *     `row_stride` elements apart (any int64, including > 2^31);
+ *   - `stream` is a hipStream_t (passed as void* so that this header needs no
+ *     HIP include); work is only enqueued on it: nothing here allocates,
+ *     synchronises or reads device memory from the host, so every call may be
+ *     captured into a HIP graph;
+ *   - the return value is ATTNRES_OK or one of the codes below; arguments are
+ *     fully checked on the host before anything is enqueued, so an invalid
+ *     call never launches a kernel.  attnres_hip_last_error() describes the
+ *     most recent failure of the calling thread.
+ *
+ * Saved tensors written by the forward and read by the backward:
+ *   out_refine[N, D] int8, low-order correction of the BF16 output: the FP32
+ *                 mix is o = bf16(o) + q * ulp(bf16(o)) / 256 to within
+ *                 ulp/512 (q = 0 for |o| < 2^-111, inf and NaN).  The
+ *                 backward needs <dO, o>; BF16 alone leaves an error that
+ *                 accumulates in dq over tokens.
+ *   logit[N, S]   FP32, already-scaled routing logit z_s per token
+ *   inv_rms[N, S] FP32, 1/r_s per token
+ *   stats[2, N]   FP32, row 0 = max_s z_s, row 1 = 1/sum_s exp(z_s - max)
+ * The two softmax statistics are kept separate on purpose: a single FP32
+ * log-sum-exp loses the normaliser when logits share an offset near 2^24.
+ */
+#ifndef ATTNRES_HIP_H
+#define ATTNRES_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum attnres_status {
+  ATTNRES_OK = 0,
+  ATTNRES_ERR_NULL_POINTER = 1,  /* a required pointer is NULL            */
+  ATTNRES_ERR_SHAPE = 2,         /* S, N, D or R outside the envelope     */
+  ATTNRES_ERR_STRIDE = 3,        /* a negative row or source stride       */
+  ATTNRES_ERR_SCALAR = 4,        /* eps not finite-positive / scale not finite */
+  ATTNRES_ERR_WORKSPACE = 5,     /* dq workspace smaller than required    */
+  ATTNRES_ERR_LAUNCH = 6,        /* the HIP runtime rejected a launch     */
+};
+
+/* Envelope (the reference's package limits, src/attnres/_sources.py:12-13). */
+#define ATTNRES_MAX_SOURCES 129
+#define ATTNRES_MAX_WIDTH 8192
+
+/* Library version string, e.g. "1.0.0". */
+const char* attnres_hip_version(void);
+
+/* Message for the calling thread's most recent non-OK status. */
+const char* attnres_hip_last_error(void);
+
+/*
+ * Packed forward.  values[s, n, :] lives at values + s*source_stride +
+ * n*row_stride.  Writes out[N, D] (contiguous BF16), out_refine[N, D]
+ * (contiguous int8) and the saved statistics.
+ *
+ * Replaces the launch inside the reference op
+ * `attnres::_fixed_tail_forward_with_aux` (src/attnres/_kernels/fixed_tail.py:904-960),
+ * i.e. `_packed_online_forward_kernel` (fixed_tail.py:244-483).
+ */
+int attnres_hip_packed_forward(const void* values, int64_t source_stride,
+                               int64_t row_stride, int64_t n_sources,
+                               int64_t n_tokens, int64_t width,
+                               const void* query, int64_t rank, float eps,
+                               float scale, void* out, int8_t* out_refine,
+                               float* logit, float* inv_rms, float* stats,
+                               void* stream);
+
+/*
+ * Number of FP32 elements the backward needs in `dq_workspace`
+ * (partial dq rows of the deterministic two-stage reduction, plus the FP32
+ * total).  Depends only on (n_tokens, width, rank); never negative for
+ * in-envelope shapes, -1 otherwise.  Host-only.
+ */
+int64_t attnres_hip_dq_workspace_elems(int64_t n_tokens, int64_t width,
+                                       int64_t rank);
+
+/*
+ * Packed backward.  Reads values (same layout as the forward), the forward's
+ * out[N, D] and out_refine[N, D] (contiguous), grad_out[N, D] (contiguous
+ * BF16) and the saved statistics; writes grad_values[S, N, D] (contiguous BF16) and
+ * grad_query[R] (BF16).  dq is reduced over all tokens in a fixed order, so it
+ * is bit-identical from run to run.
+ *
+ * Replaces `attnres::_fixed_tail_backward` (fixed_tail.py:962-1034):
+ * `_packed_online_backward_kernel` (fixed_tail.py:485-873) plus
+ * `_packed_query_reduce_kernel` (fixed_tail.py:875-899) and the BF16 cast
+ * (fixed_tail.py:1034).
+ */
+int attnres_hip_packed_backward(const void* values, int64_t source_stride,
+                                int64_t row_stride, int64_t n_sources,
+                                int64_t n_tokens, int64_t width,
+                                const void* query, int64_t rank, float scale,
+                                const void* out, const int8_t* out_refine,
+                                const void* grad_out, const float* logit,
+                                const float* inv_rms, const float* stats,
+                                void* grad_values,
+                                void* grad_query, float* dq_workspace,
+                                int64_t dq_workspace_elems, void* stream);
+
+/*
+ * Source-list forward.  `sources` and `row_strides` are HOST arrays of
+ * n_sources entries: source s, row n starts at sources[s] + n*row_strides[s].
+ * Sources are never packed or copied.  Same outputs as the packed forward.
+ *
+ * Replaces `attnres::_fixed_tail_sources_forward_with_aux`
+ * (src/attnres/_kernels/fixed_tail_sources.py:78-83), i.e.
+ * `_launch_standard_forward` / `_fla_standard_forward_kernel`
+ * (src/attnres/_kernels/fla_full_sources.py:752-804, 297-429).
+ */
+int attnres_hip_sources_forward(const void* const* sources,
+                                const int64_t* row_strides, int64_t n_sources,
+                                int64_t n_tokens, int64_t width,
+                                const void* query, int64_t rank, float eps,
+                                float scale, void* out, int8_t* out_refine,
+                                float* logit, float* inv_rms, float* stats,
+                                void* stream);
+
+/*
+ * Source-list backward.  `sources`, `row_strides` and `grad_sources` are HOST
+ * arrays of n_sources entries; grad_sources[s] is a contiguous BF16 [N, D]
+ * buffer (one per list position, even when two positions hold the same
+ * tensor: the caller's autograd adds them).
+ *
+ * Replaces `attnres::_fixed_tail_sources_backward`
+ * (fixed_tail_sources.py:85-102), i.e. `_launch_standard_backward`
+ * (fla_full_sources.py:807-894): `_fla_standard_backward_kernel` (432-629)
+ * and the dq reductions `_fla_standard_query_reduce_kernel` /
+ * `_fla_query_reduce_kernel` (632-701).
+ */
+int attnres_hip_sources_backward(const void* const* sources,
+                                 const int64_t* row_strides, int64_t n_sources,
+                                 int64_t n_tokens, int64_t width,
+                                 const void* query, int64_t rank, float scale,
+                                 const void* out, const int8_t* out_refine,
+                                 const void* grad_out, const float* logit,
+                                 const float* inv_rms, const float* stats,
+                                 void* const* grad_sources,
+                                 void* grad_query, float* dq_workspace,
+                                 int64_t dq_workspace_elems, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ATTNRES_HIP_H */

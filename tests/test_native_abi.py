@@ -1,0 +1,122 @@
+"""The C-ABI library: it loads, exports every function `include/attnres_hip.h`
+declares with the argument list the ctypes binding uses, and rejects invalid
+arguments on the host with the documented status codes before any device
+work.  Runs without a GPU (no valid call is made)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from attnres import _native
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "attnres_hip.h"
+
+_C_TYPES = {
+    "void*": ctypes.c_void_p, "const void*": ctypes.c_void_p, "float*": ctypes.c_void_p,
+    "const float*": ctypes.c_void_p, "int8_t*": ctypes.c_void_p, "const int8_t*": ctypes.c_void_p,
+    "const void* const*": ctypes.c_void_p, "void* const*": ctypes.c_void_p,
+    "const int64_t*": ctypes.c_void_p, "int64_t": ctypes.c_int64, "float": ctypes.c_float,
+}
+
+
+def _declarations() -> dict[str, list[str]]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    found = {}
+    for match in re.finditer(r"\b(?:int|int64_t|const char\*)\s+(attnres_hip_\w+)\s*\(([^)]*)\)\s*;", text):
+        name, params = match.group(1), match.group(2).strip()
+        if params in ("", "void"):
+            found[name] = []
+            continue
+        types = []
+        for param in params.split(","):
+            words = " ".join(param.split())
+            types.append(re.sub(r"\s*\b\w+$", "", words).replace(" *", "*"))
+        found[name] = types
+    return found
+
+
+def test_header_declares_the_bound_functions():
+    assert set(_declarations()) == set(_native.SIGNATURES)
+
+
+@pytest.mark.parametrize("name", sorted(_native.SIGNATURES))
+def test_binding_matches_header_argument_list(name):
+    declared = [_C_TYPES[t] for t in _declarations()[name]]
+    assert _native.SIGNATURES[name][1] == declared
+
+
+def test_library_loads_and_exports_every_symbol():
+    lib = _native.load()
+    for name in _declarations():
+        assert hasattr(lib, name), name
+    assert lib.attnres_hip_version().decode()
+
+
+def test_workspace_size_is_shape_only_and_rejects_bad_shapes():
+    lib = _native.load()
+    assert lib.attnres_hip_dq_workspace_elems(16384, 2048, 2048) > 2048
+    assert (lib.attnres_hip_dq_workspace_elems(16384, 2048, 2048)
+            == lib.attnres_hip_dq_workspace_elems(16384, 2048, 2048))
+    assert lib.attnres_hip_dq_workspace_elems(0, 2048, 2048) == -1
+    assert lib.attnres_hip_dq_workspace_elems(16, 8193, 16) == -1
+    assert lib.attnres_hip_dq_workspace_elems(16, 64, 65) == -1
+
+
+_FAKE = 0x1000  # never dereferenced: every call below fails host-side checks
+
+
+def _forward(**overrides):
+    args = dict(values=_FAKE, source_stride=64, row_stride=64, n_sources=3, n_tokens=4,
+                width=64, query=_FAKE, rank=16, eps=2.0**-23, scale=1.0, out=_FAKE,
+                out_refine=_FAKE, logit=_FAKE, inv_rms=_FAKE, stats=_FAKE, stream=None)
+    args.update(overrides)
+    return _native.load().attnres_hip_packed_forward(*args.values())
+
+
+@pytest.mark.parametrize("override,status", [
+    ({"values": None}, _native.ERR_NULL_POINTER),
+    ({"out_refine": None}, _native.ERR_NULL_POINTER),
+    ({"n_sources": 0}, _native.ERR_SHAPE),
+    ({"n_sources": 130}, _native.ERR_SHAPE),
+    ({"n_tokens": 0}, _native.ERR_SHAPE),
+    ({"width": 8193}, _native.ERR_SHAPE),
+    ({"rank": 65}, _native.ERR_SHAPE),
+    ({"rank": 0}, _native.ERR_SHAPE),
+    ({"row_stride": -1}, _native.ERR_STRIDE),
+    ({"eps": 0.0}, _native.ERR_SCALAR),
+    ({"eps": float("nan")}, _native.ERR_SCALAR),
+    ({"scale": float("inf")}, _native.ERR_SCALAR),
+])
+def test_packed_forward_rejects_invalid_arguments(override, status):
+    assert _forward(**override) == status
+    assert _native.load().attnres_hip_last_error().decode()
+
+
+def test_backward_rejects_a_short_workspace():
+    lib = _native.load()
+    need = lib.attnres_hip_dq_workspace_elems(4, 64, 16)
+    status = lib.attnres_hip_packed_backward(
+        _FAKE, 64, 64, 3, 4, 64, _FAKE, 16, 1.0, _FAKE, _FAKE, _FAKE, _FAKE, _FAKE, _FAKE,
+        _FAKE, _FAKE, _FAKE, need - 1, None)
+    assert status == _native.ERR_WORKSPACE
+    assert b"workspace" in lib.attnres_hip_last_error()
+
+
+def test_source_list_rejects_null_entries():
+    lib = _native.load()
+    pointers = (ctypes.c_void_p * 2)(_FAKE, None)
+    strides = (ctypes.c_int64 * 2)(64, 64)
+    status = lib.attnres_hip_sources_forward(
+        pointers, strides, 2, 4, 64, _FAKE, 16, 2.0**-23, 1.0, _FAKE, _FAKE, _FAKE, _FAKE,
+        _FAKE, None)
+    assert status == _native.ERR_NULL_POINTER
+
+
+def test_status_is_raised_with_the_library_message():
+    _forward(width=9000)
+    with pytest.raises(ValueError, match="width"):
+        _native.check(_native.ERR_SHAPE, "attnres packed forward")
