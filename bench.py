@@ -17,9 +17,11 @@ bandwidth of the whole read in TB/s (bytes below / measured time per read);
     forward  = S*N*D*2 (values read) + N*D*2 (output write)
     backward = S*N*D*2 (values read) + N*D*2 (dO read) + S*N*D*2 (dvalues write)
 
-``roofline`` describes the dominant launch (the backward op: the fused
-backward kernel plus the dq finalisation kernel), timed with HIP events
-recorded on the stream the kernels run on.  ``cpu_baseline`` times the CPU
+``roofline`` describes the dominant launch, the backward op (the fused
+backward kernel and the two kernels of the deterministic dq reduction),
+timed with HIP events recorded on the stream the kernels run on; its
+``traffic`` is the HBM bytes per launch measured with rocprofv3 counters
+(profiles/attnres_<config>_hbm_traffic.json).  ``cpu_baseline`` times the CPU
 FP32 oracle (test infrastructure under ``oracle/``) on the host over a
 bounded sample of the same inputs.
 
@@ -77,6 +79,16 @@ def make_inputs(cfg: dict, device, seed: int = 0):
     query = (torch.randn(rank, generator=generator, device=device) / math.sqrt(rank)).to(torch.bfloat16)
     grad_out = torch.randn(shape[1:], generator=generator, device=device).to(torch.bfloat16)
     return values, query, grad_out
+
+
+def measured_traffic(config: str, key: str) -> int | None:
+    """HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
+    counters (calibrated against a device copy of known size), as recorded in
+    profiles/attnres_<config>_hbm_traffic.json; None when not measured."""
+    path = ROOT / "profiles" / f"attnres_{config}_hbm_traffic.json"
+    if not path.is_file():
+        return None
+    return int(json.loads(path.read_text()).get(key)) or None
 
 
 def copy_probe(gib: float = 1.0, reps: int = 5) -> None:
@@ -230,9 +242,12 @@ def main(argv=None) -> int:
                     "pct_of_peak": round(100 * fwd_tbs / HBM_PEAK_TBS, 2)},
         "backward": {"us": round(bwd_avg * 1e3, 2), "bytes": bwd_bytes, "TB/s": round(bwd_tbs, 4),
                      "pct_of_peak": round(100 * bwd_tbs / HBM_PEAK_TBS, 2)},
-        "roofline": {"bound": "hbm", "kernel": "attnres_bwd_kernel + attnres_dq_finalize_kernel",
+        "roofline": {"bound": "hbm",
+                     "kernel": "backward op: attnres_bwd_kernel + attnres_dq_slices_kernel + "
+                               "attnres_dq_finalize_kernel",
                      "achieved": round(bwd_tbs * 1e3, 1), "peak": HBM_PEAK_TBS * 1e3,
-                     "unit": "GB/s", "frac": round(bwd_tbs / HBM_PEAK_TBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(bwd_tbs / HBM_PEAK_TBS, 4),
+                     "traffic": measured_traffic(args.config, "backward_bytes")},
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:

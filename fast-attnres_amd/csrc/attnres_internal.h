@@ -1,0 +1,159 @@
+// attnres_internal.h - types shared by the C ABI (attnres_hip.hip) and the
+// kernels (attnres_kernels.hip, compiled once per row geometry).
+//
+// A token row of width D is owned by a group of `lanes` threads; each lane
+// holds `chunks` 16-byte chunks (8 BF16 elements) of the row.  The kernels of
+// one geometry are instantiated in their own translation unit, so the
+// geometries build in parallel.
+#ifndef ATTNRES_INTERNAL_H
+#define ATTNRES_INTERNAL_H
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "attnres_hip.h"
+
+namespace attnres_hip {
+
+constexpr int kMaxSources = ATTNRES_MAX_SOURCES;
+constexpr int kMaxWidth = ATTNRES_MAX_WIDTH;
+constexpr int kBlock = 256;           // threads per workgroup (4 wavefronts)
+constexpr int kVec = 8;               // BF16 elements per chunk (16 bytes)
+constexpr int kMaxGridBlocks = 2048;  // persistent grid cap
+constexpr int kFinalizeSlices = 64;   // first-stage slices of the dq reduction
+
+// ---------------------------------------------------------------- addressing
+
+// Packed [S, N, D] values: row (s, n) at base + s*source_stride + n*row_stride.
+struct PackedRows {
+  const uint16_t* base;
+  int64_t source_stride;
+  int64_t row_stride;
+  __device__ __forceinline__ const uint16_t* row(int s, int64_t n) const {
+    return base + s * source_stride + n * row_stride;
+  }
+};
+
+// Ordered source list: one base pointer and row stride per list position.
+struct ListRows {
+  const uint16_t* ptr[kMaxSources];
+  int64_t row_stride[kMaxSources];
+  __device__ __forceinline__ const uint16_t* row(int s, int64_t n) const {
+    return ptr[s] + n * row_stride[s];
+  }
+};
+
+// Gradients of a packed input: one contiguous [S, N, D] buffer.
+struct PackedGrads {
+  uint16_t* base;
+  int64_t source_stride;  // N * D
+  __device__ __forceinline__ uint16_t* row(int s, int64_t n, int d) const {
+    return base + s * source_stride + n * d;
+  }
+};
+
+// Gradients of a source list: one contiguous [N, D] buffer per position.
+struct ListGrads {
+  uint16_t* ptr[kMaxSources];
+  __device__ __forceinline__ uint16_t* row(int s, int64_t n, int d) const {
+    return ptr[s] + n * d;
+  }
+};
+
+template <class Rows>
+struct FwdArgs {
+  Rows src;
+  const uint16_t* query;  // [R] BF16, contiguous
+  uint16_t* out;          // [N, D] BF16, contiguous
+  int8_t* out_refine;     // [N, D] low-order correction of out
+  float* logit;           // [N, S]
+  float* inv_rms;         // [N, S]
+  float* stats;           // [2, N]
+  int64_t n_tokens;
+  int n_sources;
+  int width;
+  int rank;
+  float eps;
+  float scale;
+};
+
+template <class Rows, class Grads>
+struct BwdArgs {
+  Rows src;
+  Grads grad;
+  const uint16_t* query;
+  const uint16_t* out;       // [N, D] BF16 forward output, contiguous
+  const int8_t* out_refine;  // [N, D] its low-order correction
+  const uint16_t* grad_out;  // [N, D] BF16, contiguous
+  const float* logit;
+  const float* inv_rms;
+  const float* stats;
+  float* partial;            // [gridDim.x, R] FP32 dq partial rows
+  int64_t n_tokens;
+  int n_sources;
+  int width;
+  int rank;
+  float scale;
+};
+
+// ------------------------------------------------------------------ geometry
+
+struct Geometry {
+  int lanes;   // threads per token group
+  int chunks;  // 16-byte chunks per lane
+};
+
+// The smallest group that covers D: 16/32/64 lanes (one or several tokens per
+// wavefront, no barriers) up to D = 4096, one workgroup per token beyond.
+inline Geometry geometry(int64_t D) {
+  if (D <= 16 * kVec) return {16, 1};
+  if (D <= 32 * kVec) return {32, 1};
+  if (D <= 64 * kVec) return {64, 1};
+  if (D <= 128 * kVec) return {64, 2};
+  if (D <= 256 * kVec) return {64, 4};
+  if (D <= 512 * kVec) return {64, 8};
+  return {256, 4};
+}
+
+// Masks can be skipped when every lane position is an in-range key coordinate.
+inline bool no_mask(const Geometry& geo, int64_t width, int64_t rank) {
+  return rank == width && width == static_cast<int64_t>(geo.lanes) * geo.chunks * kVec;
+}
+
+// Persistent grid: one group per token at most, capped by the workgroups that
+// stay resident on the device (`resident` <= 0: unknown) and kMaxGridBlocks.
+inline int64_t grid_blocks(int64_t N, int64_t D, int64_t resident) {
+  const int64_t groups = kBlock / geometry(D).lanes;
+  int64_t blocks = (N + groups - 1) / groups;
+  if (resident > 0 && blocks > resident) blocks = resident;
+  return blocks < kMaxGridBlocks ? blocks : kMaxGridBlocks;
+}
+
+// ----------------------------------------------------------------- launchers
+// Defined in attnres_kernels.hip, one explicit instantiation per geometry.
+
+// Enqueue the forward of geometry (G, CH) on `stream`.
+template <int G, int CH, class Rows>
+void launch_fwd_geometry(const FwdArgs<Rows>& a, bool nomask, bool vec, hipStream_t stream);
+
+// Enqueue the backward of geometry (G, CH); returns the grid size (the number
+// of dq partial rows written to a.partial).
+template <int G, int CH, class Rows, class Grads>
+int64_t launch_bwd_geometry(const BwdArgs<Rows, Grads>& a, bool nomask, bool vec, hipStream_t stream);
+
+#define ATTNRES_DECLARE_GEOMETRY(G, CH)                                                                  \
+  extern template void launch_fwd_geometry<G, CH, PackedRows>(const FwdArgs<PackedRows>&, bool, bool,    \
+                                                              hipStream_t);                              \
+  extern template void launch_fwd_geometry<G, CH, ListRows>(const FwdArgs<ListRows>&, bool, bool,        \
+                                                            hipStream_t);                                \
+  extern template int64_t launch_bwd_geometry<G, CH, PackedRows, PackedGrads>(                           \
+      const BwdArgs<PackedRows, PackedGrads>&, bool, bool, hipStream_t);                                 \
+  extern template int64_t launch_bwd_geometry<G, CH, ListRows, ListGrads>(                               \
+      const BwdArgs<ListRows, ListGrads>&, bool, bool, hipStream_t);
+
+#define ATTNRES_FOR_EACH_GEOMETRY(X) X(16, 1) X(32, 1) X(64, 1) X(64, 2) X(64, 4) X(64, 8) X(256, 4)
+
+}  // namespace attnres_hip
+
+#endif  // ATTNRES_INTERNAL_H

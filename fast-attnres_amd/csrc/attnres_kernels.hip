@@ -1,0 +1,851 @@
+// attnres_kernels.hip - gfx950 kernels of the Fast-AttnRes read.
+//
+// Compiled once per row geometry (ATTNRES_LANES, ATTNRES_CHUNKS); the C ABI
+// in attnres_hip.hip dispatches to the instantiations declared in
+// attnres_internal.h.
+//
+// The read is a bandwidth-bound reduction over S depth sources: every value
+// byte is touched once in the forward and once in the backward, so both
+// kernels are single streaming passes over HBM with FP32 register state and
+// no MFMA (arithmetic intensity is ~3 FP32 flop/byte).
+//
+// Work decomposition.  A "token group" of G lanes owns one token row; each
+// lane owns CH chunks of 8 consecutive BF16 elements (one 16-byte load), the
+// chunks of a row interleaved across the group so that one load instruction
+// of a wavefront reads a contiguous span:
+//     element d of chunk c, lane l:  d = (c*G + l)*8 + e,  e in [0, 8).
+// G is 16/32/64 (one or several tokens per wavefront; sums over the group are
+// DPP butterflies inside 16-lane rows plus lane reads across rows) or 256
+// (one token per workgroup for D > 4096; the four wave sums meet in LDS).
+//
+// Forward.  Per token, the S source rows stream through a ring of NB rows
+// held in registers (NB loads in flight per group).  For each source the
+// packed BF16 words feed v_dot2_f32_bf16 for the key sum of squares and the
+// query dot; the online softmax (running max, running sum, FP32 accumulator
+// of the full row) is updated; the per-source logit and 1/rms and the
+// per-token (max, 1/sum) are saved for the backward.
+//
+// Backward.  The N*S (token, source) items are split into equal contiguous
+// ranges, one per group of a persistent grid, so every group streams the
+// same number of rows.  The ring of value rows crosses token boundaries;
+// at each new token the group loads dO and the saved output (BF16 plus one
+// refinement byte per element, see refine_encode) and forms
+// delta = <dO, o>.  Per item: dw = <v, dO>, p = exp(z - max) / sum,
+// dz = p (dw - delta), and
+//     dv = p dO + [key coords] (a q + b v),  a = scale dz / r,  b = -dz z / (R r^2)
+// folded in FP32 and stored once as BF16.  dq = sum scale dz k accumulates in
+// registers; each workgroup reduces its groups in LDS in a fixed order to
+// one partial row, and two small kernels sum the partial rows in a fixed
+// order, so dq is bit-reproducible run to run.
+//
+// Reference behaviour followed: src/attnres/_kernels/fixed_tail.py:244-483
+// (forward), :485-873 (backward), :875-899 (dq reduction); the list layout of
+// src/attnres/_kernels/fla_full_sources.py:164-214, 297-629.
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+
+#include "attnres_internal.h"
+
+namespace attnres_hip {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// ------------------------------------------------------------- BF16 helpers
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Two FP32 values to packed BF16, round-to-nearest-even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  f32x2 v = {lo, hi};
+  bf16x2 b = __builtin_convertvector(v, bf16x2);
+  return __builtin_bit_cast(uint32_t, b);
+}
+
+// acc + a.lo*b.lo + a.hi*b.hi on packed BF16 pairs (v_dot2_f32_bf16): the
+// products are exact in FP32 and the sum is rounded as an FP32 addition.
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
+                                         __builtin_bit_cast(bf16x2, b), acc, false);
+}
+
+template <int G>
+__device__ __forceinline__ int chunk_start(int c, int lane) { return (c * G + lane) * kVec; }
+
+// Load one row (this lane's chunks) as raw packed BF16 words.  Every load is
+// unconditional: a chunk that starts at or beyond D reads the row's first
+// chunk instead, and callers neutralise such lanes with the word masks of
+// key_masks / range_masks (branch-free loads keep several rows in flight;
+// a conditional load would join control flow and force a wait for it).
+// VEC requires 16-byte aligned rows and D % 8 == 0 (so D >= 8).
+template <int G, int CH, bool VEC>
+__device__ __forceinline__ void load_row(const uint16_t* __restrict__ row, int lane, int D,
+                                         u32x4 (&raw)[CH]) {
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int d0 = chunk_start<G>(c, lane);
+    if constexpr (VEC) {
+      const int at = d0 < D ? d0 : 0;
+      raw[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(row + at));
+    } else {
+      uint32_t w[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d = d0 + 2 * j;
+        const uint32_t lo = row[d < D ? d : D - 1];
+        const uint32_t hi = row[d + 1 < D ? d + 1 : D - 1];
+        w[j] = lo | (hi << 16);
+      }
+      raw[c] = u32x4{w[0], w[1], w[2], w[3]};
+    }
+  }
+}
+
+template <bool VEC>
+__device__ __forceinline__ void store_chunk(uint16_t* __restrict__ row, int d0, int D, const u32x4& w) {
+  if constexpr (VEC) {
+    __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(row + d0));
+  } else {
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) {
+      if (d0 + e < D) {
+        row[d0 + e] = static_cast<uint16_t>((e & 1) ? (ws[e >> 1] >> 16) : (ws[e >> 1] & 0xffffu));
+      }
+    }
+  }
+}
+
+// Output refinement.  The backward needs delta = <dO, o> with the FP32 mix o;
+// the BF16 output alone leaves a per-token error in delta that accumulates
+// in dq over tokens.  The forward therefore also stores one signed byte per
+// element: o - bf16(o) in units of ulp(bf16(o))/256 (|o - bf16(o)| <= ulp/2
+// under round-to-nearest-even).  Decoding bf16 + q*unit is exact in FP32 and
+// recovers o to ulp/512 -- 256x tighter than the BF16 output, at one byte
+// per element instead of an FP32 copy's four.  Exponent fields below 16
+// (|o| < 2^-111), infinities and NaNs carry no correction.
+__device__ __forceinline__ int refine_encode(float o, uint32_t bf16_bits) {
+  const int e = static_cast<int>((bf16_bits >> 7) & 0xffu);
+  const float rounded = __uint_as_float(bf16_bits << 16);
+  // 2^(142-e) for 16 <= e <= 254; the clamped exponent keeps the factor a
+  // normal float for every e, and the select below drops the other cases.
+  const int ec = min(max(e, 16), 254);
+  const float inv_unit = __uint_as_float(static_cast<uint32_t>(269 - ec) << 23);
+  const float t = fminf(fmaxf(rintf((o - rounded) * inv_unit), -127.0f), 127.0f);
+  return (e >= 16 && e <= 254) ? static_cast<int>(t) : 0;
+}
+
+// Store this lane's chunks of a BF16 row and of its refinement bytes.
+template <int G, int CH, bool NOMASK, bool VEC>
+__device__ __forceinline__ void store_row_refined(uint16_t* __restrict__ row, int8_t* __restrict__ refine,
+                                                  int lane, int D, const float (&x)[CH][kVec]) {
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int d0 = chunk_start<G>(c, lane);
+    if (!NOMASK && d0 >= D) continue;
+    uint32_t w[4];
+    uint32_t r[2] = {0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      w[j] = pack_bf16x2(x[c][2 * j], x[c][2 * j + 1]);
+      const uint32_t q0 = static_cast<uint32_t>(refine_encode(x[c][2 * j], w[j] & 0xffffu)) & 0xffu;
+      const uint32_t q1 = static_cast<uint32_t>(refine_encode(x[c][2 * j + 1], w[j] >> 16)) & 0xffu;
+      r[j >> 1] |= (q0 | (q1 << 8)) << (16 * (j & 1));
+    }
+    store_chunk<VEC>(row, d0, D, u32x4{w[0], w[1], w[2], w[3]});
+    if constexpr (VEC) {
+      __builtin_nontemporal_store(u32x2{r[0], r[1]}, reinterpret_cast<u32x2*>(refine + d0));
+    } else {
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) {
+        if (d0 + e < D) refine[d0 + e] = static_cast<int8_t>((r[e >> 2] >> (8 * (e & 3))) & 0xffu);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // encode one chunk at a time (register pressure)
+  }
+}
+
+// Query words on this lane's row positions: packed BF16 q[d - (D-R)] on the
+// key coordinates, +0 elsewhere (including d >= D).  The loads are
+// unconditional (clamped index) and masked afterwards, so none of them sits
+// behind a branch.
+template <int G, int CH>
+__device__ __forceinline__ void load_query_words(const uint16_t* __restrict__ query, int lane, int D,
+                                                 int tail0, uint32_t (&qw)[CH][4]) {
+  const int R = D - tail0;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d = chunk_start<G>(c, lane) + 2 * j;
+      const uint32_t lo = query[min(max(d - tail0, 0), R - 1)];
+      const uint32_t hi = query[min(max(d + 1 - tail0, 0), R - 1)];
+      const uint32_t mask = ((d >= tail0 && d < D) ? 0x0000ffffu : 0u) |
+                            ((d + 1 >= tail0 && d + 1 < D) ? 0xffff0000u : 0u);
+      qw[c][j] = (lo | (hi << 16)) & mask;
+    }
+  }
+}
+
+// Word masks selecting the key coordinates (D-R <= d < D) of this lane's words.
+template <int G, int CH>
+__device__ __forceinline__ void key_masks(int lane, int D, int tail0, uint32_t (&km)[CH][4]) {
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d = chunk_start<G>(c, lane) + 2 * j;
+      km[c][j] = ((d >= tail0 && d < D) ? 0x0000ffffu : 0u) |
+                 ((d + 1 >= tail0 && d + 1 < D) ? 0xffff0000u : 0u);
+    }
+  }
+}
+
+// Zero the words of this lane's chunks that lie at or beyond D.
+template <int G, int CH>
+__device__ __forceinline__ void mask_range(int lane, int D, u32x4 (&x)[CH]) {
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int d = chunk_start<G>(c, lane);
+    x[c].x &= (d < D ? 0x0000ffffu : 0u) | (d + 1 < D ? 0xffff0000u : 0u);
+    x[c].y &= (d + 2 < D ? 0x0000ffffu : 0u) | (d + 3 < D ? 0xffff0000u : 0u);
+    x[c].z &= (d + 4 < D ? 0x0000ffffu : 0u) | (d + 5 < D ? 0xffff0000u : 0u);
+    x[c].w &= (d + 6 < D ? 0x0000ffffu : 0u) | (d + 7 < D ? 0xffff0000u : 0u);
+  }
+}
+
+// --------------------------------------------------------------- reductions
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float lane_value(float x, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
+}
+
+// Sum over the W lanes of a token group inside one wavefront (W = 16, 32 or
+// 64, groups aligned to W).  DPP quad permutations and row mirrors sum each
+// 16-lane row; rows are combined from lane reads.  Every lane of the group
+// receives the same bits: each step adds a pair of partial sums that all
+// receiving lanes see in one of the two orders of a commutative add.
+template <int W>
+__device__ __forceinline__ float wave_sum(float x) {
+  x += dpp<0xb1>(x);   // quad_perm [1,0,3,2]
+  x += dpp<0x4e>(x);   // quad_perm [2,3,0,1]
+  x += dpp<0x141>(x);  // row_half_mirror
+  x += dpp<0x140>(x);  // row_mirror
+  if constexpr (W == 16) {
+    return x;
+  } else if constexpr (W == 32) {
+    const float lo = lane_value(x, 0) + lane_value(x, 16);
+    const float hi = lane_value(x, 32) + lane_value(x, 48);
+    return (threadIdx.x & 32) ? hi : lo;
+  } else {
+    static_assert(W == 64, "group width");
+    return (lane_value(x, 0) + lane_value(x, 16)) + (lane_value(x, 32) + lane_value(x, 48));
+  }
+}
+
+// Sum NV values over the G lanes of a token group.  For G > 64 the group is
+// the whole workgroup: the wave sums meet in LDS (every thread must make the
+// same sequence of calls; `xred` holds two alternating slot sets so one
+// barrier per call suffices).
+template <int G, int NV>
+__device__ __forceinline__ void group_sum(float (&x)[NV], float* xred, int& phase) {
+#pragma unroll
+  for (int i = 0; i < NV; ++i) x[i] = wave_sum<(G < 64 ? G : 64)>(x[i]);
+  if constexpr (G > 64) {
+    constexpr int kWaves = G / 64;
+    const int wave = threadIdx.x / 64;
+    float* slot = xred + phase * kWaves * NV;
+    if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) slot[wave * NV + i] = x[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      float t = slot[i];
+#pragma unroll
+      for (int w = 1; w < kWaves; ++w) t += slot[w * NV + i];
+      x[i] = t;
+    }
+    phase ^= 1;
+  }
+}
+
+template <int G>
+constexpr int xred_floats(int nv) {
+  return G > 64 ? 2 * (G / 64) * nv : 1;
+}
+
+// ------------------------------------------------------------------ forward
+
+// Index of this thread's token group.  For G >= 64 a group is one or more
+// whole wavefronts, and readfirstlane tells the compiler so: group-level
+// cursors, loop bounds and branches then live in scalar registers.
+template <int G>
+__device__ __forceinline__ int group_index() {
+  if constexpr (G >= 64) {
+    return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / G);
+  } else {
+    return static_cast<int>(threadIdx.x) / G;
+  }
+}
+
+// Contiguous share [first, last) of `count` work units for group `gid` of
+// `groups` (shares differ in size by at most one unit).
+__device__ __forceinline__ void share(int64_t count, int64_t gid, int64_t groups, int64_t& first,
+                                      int64_t& last) {
+  first = gid * count / groups;
+  last = (gid + 1) * count / groups;
+}
+
+// Cursor over (token, source) items in token-major order.
+struct ItemCursor {
+  int64_t token;
+  int source;
+  __device__ __forceinline__ void advance(int S) {
+    if (++source == S) {
+      source = 0;
+      ++token;
+    }
+  }
+};
+
+// Refill a ring slot with the row of `at`, or -- past the end of the range --
+// with a load every lane points at one live address (a single cache line), so
+// that each slot is refilled unconditionally: a conditional refill would make
+// the compiler wait for all outstanding loads before every slot is used.
+template <int G, int CH, bool VEC, class Rows>
+__device__ __forceinline__ void refill(const Rows& src, const ItemCursor& at, bool live, const uint16_t* idle,
+                                       int lane, int D, u32x4 (&slot)[CH]) {
+  if constexpr (VEC) {
+    const uint16_t* row = live ? src.row(at.source, at.token) : idle;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int d0 = chunk_start<G>(c, lane);
+      const int offset = (live && d0 < D) ? d0 : 0;
+      slot[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(row + offset));
+    }
+  } else {
+    load_row<G, CH, VEC>(live ? src.row(at.source, at.token) : idle, lane, D, slot);
+  }
+}
+
+// NOMASK: R == D and D == G*CH*8, so every lane position is an in-range key
+// coordinate and no word masks are needed.
+//
+// Persistent: each group owns a contiguous range of tokens and streams their
+// S*tokens rows through the ring without draining it between tokens.
+template <int G, int CH, int NB, bool NOMASK, bool VEC, class Rows>
+__global__ void __launch_bounds__(kBlock) attnres_fwd_kernel(const FwdArgs<Rows> a) {
+  static_assert(G <= 64 || G == kBlock, "a wide group is the whole workgroup");
+  constexpr int kGroups = kBlock / G;
+  __shared__ float xred[xred_floats<G>(2)];
+  const int lane = threadIdx.x % G;
+  const int group = group_index<G>();
+  const int D = a.width;
+  const int tail0 = D - a.rank;
+  const int S = a.n_sources;
+  const float inv_R = 1.0f / static_cast<float>(a.rank);
+  int phase = 0;
+
+  int64_t t_first, t_last;
+  share(a.n_tokens, static_cast<int64_t>(blockIdx.x) * kGroups + group,
+        static_cast<int64_t>(gridDim.x) * kGroups, t_first, t_last);
+  if (t_first >= t_last) return;  // whole group idle (no barrier follows for it)
+
+  uint32_t qw[CH][4];
+  load_query_words<G, CH>(a.query, lane, D, tail0, qw);
+  uint32_t km[CH][4];
+  if constexpr (!NOMASK) key_masks<G, CH>(lane, D, tail0, km);
+
+  const int64_t last = t_last * S;
+  const uint16_t* idle = a.src.row(0, t_first);
+  ItemCursor ahead{t_first, 0};
+  int64_t ahead_item = t_first * S;
+  u32x4 ring[NB][CH];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const bool live = ahead_item < last;
+    refill<G, CH, VEC>(a.src, ahead, live, idle, lane, D, ring[j]);
+    if (live) {
+      ++ahead_item;
+      ahead.advance(S);
+    }
+  }
+
+  // acc needs no reset between tokens: with run_max = -inf the first
+  // source of a token rescales the old (finite) contents by exp(-inf) = 0.
+  float acc[CH][kVec];
+#pragma unroll
+  for (int c = 0; c < CH; ++c)
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) acc[c][e] = 0.0f;
+  float run_max = -INFINITY;
+  float run_sum = 0.0f;
+  ItemCursor at{t_first, 0};
+
+  // One item: the row in ring slot j.  `refill_slot` is false only in the
+  // remainder after the last full round, where every row is already loaded.
+  auto step = [&](int j, bool refill_slot) __attribute__((always_inline)) {
+    const int s = at.source;
+    const int64_t token = at.token;
+    float red[2] = {0.0f, 0.0f};  // key sum of squares, <key, q>
+    {
+      float ss1 = 0.0f, qd1 = 0.0f;
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const uint32_t w[4] = {ring[j][c].x, ring[j][c].y, ring[j][c].z, ring[j][c].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t kw = NOMASK ? w[k] : (w[k] & km[c][k]);
+          if (k & 1) {
+            ss1 = dot2(kw, kw, ss1);
+            qd1 = dot2(kw, qw[c][k], qd1);
+          } else {
+            red[0] = dot2(kw, kw, red[0]);
+            red[1] = dot2(kw, qw[c][k], red[1]);
+          }
+        }
+      }
+      red[0] += ss1;
+      red[1] += qd1;
+    }
+    group_sum<G, 2>(red, xred, phase);
+    const float inv_rms = rsqrtf(fmaf(red[0], inv_R, a.eps));
+    const float z = red[1] * inv_rms * a.scale;
+
+    // Online softmax.  A new maximum first rescales the accumulator in place
+    // (a group-uniform branch taken on the sources that raise the maximum);
+    // then every source adds exp(z - max) * v with one FMA per element.  A
+    // single update path keeps the accumulator in one set of registers.
+    if (z > run_max) {
+      const float alpha = __expf(run_max - z);  // 0 for the first source of a token
+      run_sum *= alpha;
+      run_max = z;
+#pragma unroll
+      for (int c = 0; c < CH; ++c)
+#pragma unroll
+        for (int e = 0; e < kVec; ++e) acc[c][e] *= alpha;
+    }
+    {
+      const float w = __expf(z - run_max);
+      run_sum += w;
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const uint32_t wd[4] = {ring[j][c].x, ring[j][c].y, ring[j][c].z, ring[j][c].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          acc[c][2 * k] = fmaf(w, bf16_lo(wd[k]), acc[c][2 * k]);
+          acc[c][2 * k + 1] = fmaf(w, bf16_hi(wd[k]), acc[c][2 * k + 1]);
+        }
+      }
+    }
+    if (lane == 0) {
+      a.logit[token * S + s] = z;
+      a.inv_rms[token * S + s] = inv_rms;
+    }
+
+    if (refill_slot) {
+      // The slot is refilled only after its last use: without the barrier the
+      // scheduler hoists the load and keeps two copies of the slot live.
+      __builtin_amdgcn_sched_barrier(0);
+      const bool live = ahead_item < last;
+      refill<G, CH, VEC>(a.src, ahead, live, idle, lane, D, ring[j]);
+      if (live) {
+        ++ahead_item;
+        ahead.advance(S);
+      }
+    }
+
+    if (s == S - 1) {  // token complete: normalise and store the output row
+      // Normalised in place: the next token's first source rescales acc by 0.
+      const float inv_sum = 1.0f / run_sum;
+#pragma unroll
+      for (int c = 0; c < CH; ++c)
+#pragma unroll
+        for (int e = 0; e < kVec; ++e) acc[c][e] *= inv_sum;
+      store_row_refined<G, CH, NOMASK, VEC>(a.out + token * D, a.out_refine + token * D, lane, D, acc);
+      if (lane == 0) {
+        a.stats[token] = run_max;
+        a.stats[a.n_tokens + token] = inv_sum;
+      }
+      run_max = -INFINITY;
+      run_sum = 0.0f;
+    }
+    at.advance(S);
+  };
+
+  // Full rounds refill every slot (with an idle load past the end), so the
+  // loop body has no exit test between slots: any such path back to the loop
+  // head would make the compiler wait there for all outstanding loads.
+  const int64_t items = last - t_first * S;
+  const int64_t rounds = items / NB;
+  const int rem = static_cast<int>(items - rounds * NB);
+  for (int64_t r = 0; r < rounds; ++r) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) step(j, true);
+  }
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    if (j < rem) step(j, false);
+  }
+}
+
+// ----------------------------------------------------------------- backward
+
+// What the backward needs per token besides the value rows: dO (packed BF16),
+// the saved output and its refinement bytes (for delta = <dO, o>) and the
+// softmax statistics.
+template <int CH>
+struct TokenRows {
+  u32x4 g[CH];
+  u32x4 o[CH];
+  u32x2 r[CH];
+  float run_max;
+  float inv_sum;
+};
+
+template <int G, int CH, bool VEC, class Rows, class Grads>
+__device__ __forceinline__ void load_token(const BwdArgs<Rows, Grads>& a, int64_t token, int lane,
+                                           TokenRows<CH>& t) {
+  const int D = a.width;
+  load_row<G, CH, VEC>(a.grad_out + token * D, lane, D, t.g);
+  load_row<G, CH, VEC>(a.out + token * D, lane, D, t.o);
+  const int8_t* refine = a.out_refine + token * D;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int d0 = chunk_start<G>(c, lane);
+    if constexpr (VEC) {
+      t.r[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(refine + (d0 < D ? d0 : 0)));
+    } else {
+      uint32_t rq[2] = {0u, 0u};
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) {
+        const uint32_t b = static_cast<uint8_t>(refine[d0 + e < D ? d0 + e : D - 1]);
+        rq[e >> 2] |= b << (8 * (e & 3));
+      }
+      t.r[c] = u32x2{rq[0], rq[1]};
+    }
+  }
+  t.run_max = a.stats[token];
+  t.inv_sum = a.stats[a.n_tokens + token];
+}
+
+// Low-order part of a refined output element: q * ulp(bf16)/256 (see
+// refine_encode), exactly 0 when q == 0.
+__device__ __forceinline__ float refine_delta(uint32_t bf16_bits, int q) {
+  const int e = static_cast<int>((bf16_bits >> 7) & 0xffu);
+  const float unit = __uint_as_float(static_cast<uint32_t>(min(max(e, 16), 254) - 15) << 23);
+  return (e >= 16 && e <= 254) ? static_cast<float>(q) * unit : 0.0f;
+}
+
+// delta = <dO, o> over this lane's elements (dO already zero beyond D).  The
+// BF16 part of o goes through the same dot2 sequence as dw = <v, dO>, and the
+// refinement is added last: when o equals a source row exactly (one source,
+// or identical sources) delta and dw are then bitwise equal and
+// dz = p (dw - delta) is exactly zero, as in the oracle.
+template <int CH>
+__device__ __forceinline__ float token_delta(const TokenRows<CH>& t) {
+  float m0 = 0.0f, m1 = 0.0f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    m0 = dot2(t.o[c].x, t.g[c].x, m0);
+    m1 = dot2(t.o[c].y, t.g[c].y, m1);
+    m0 = dot2(t.o[c].z, t.g[c].z, m0);
+    m1 = dot2(t.o[c].w, t.g[c].w, m1);
+  }
+  float corr = 0.0f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const uint32_t w[4] = {t.o[c].x, t.o[c].y, t.o[c].z, t.o[c].w};
+    const uint32_t gw[4] = {t.g[c].x, t.g[c].y, t.g[c].z, t.g[c].w};
+    const uint32_t rq[2] = {t.r[c].x, t.r[c].y};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int q0 = static_cast<int8_t>((rq[j >> 1] >> (16 * (j & 1))) & 0xffu);
+      const int q1 = static_cast<int8_t>((rq[j >> 1] >> (16 * (j & 1) + 8)) & 0xffu);
+      corr = fmaf(refine_delta(w[j] & 0xffffu, q0), bf16_lo(gw[j]), corr);
+      corr = fmaf(refine_delta(w[j] >> 16, q1), bf16_hi(gw[j]), corr);
+    }
+  }
+  return (m0 + m1) + corr;
+}
+
+// Persistent: the N*S items are split into equal contiguous ranges, one per
+// group, and the value rows stream through the ring across token
+// boundaries.  The next token's dO, output, refinement bytes and statistics
+// are requested `lead` = min(NB, S) items before the current token ends,
+// right after a ring refill, and folded into delta on the token's last item
+// -- when the younger rows in the ring are still in flight -- so a token
+// switch does not drain the ring.
+template <int G, int CH, int NB, bool NOMASK, bool VEC, class Rows, class Grads>
+__global__ void __launch_bounds__(kBlock) attnres_bwd_kernel(const BwdArgs<Rows, Grads> a) {
+  static_assert(G <= 64 || G == kBlock, "a wide group is the whole workgroup");
+  constexpr int kGroups = kBlock / G;
+  __shared__ float xred[xred_floats<G>(1)];
+  __shared__ float dq_lds[kGroups * G * kVec];
+  // The query on row positions, FP32, +0 off the key: read per item from LDS
+  // (no registers; every group of the workgroup shares it).
+  __shared__ __attribute__((aligned(16))) float q_lds[G * CH * kVec];
+  const int lane = threadIdx.x % G;
+  const int group = group_index<G>();
+  const int D = a.width;
+  const int R = a.rank;
+  const int tail0 = D - R;
+  const int S = a.n_sources;
+  const float inv_R = 1.0f / static_cast<float>(R);
+  const float scale = a.scale;
+  int phase = 0;
+
+  for (int d = threadIdx.x; d < G * CH * kVec; d += kBlock) {
+    const uint32_t bits = a.query[min(max(d - tail0, 0), R - 1)];
+    q_lds[d] = (d >= tail0 && d < D) ? __uint_as_float(bits << 16) : 0.0f;
+  }
+  __syncthreads();
+  uint32_t km[CH][4];
+  if constexpr (!NOMASK) key_masks<G, CH>(lane, D, tail0, km);
+  float dq[CH][kVec];
+#pragma unroll
+  for (int c = 0; c < CH; ++c)
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) dq[c][e] = 0.0f;
+
+  int64_t first, last;
+  share(a.n_tokens * S, static_cast<int64_t>(blockIdx.x) * kGroups + group,
+        static_cast<int64_t>(gridDim.x) * kGroups, first, last);
+
+  if (first < last) {
+    const int64_t last_token = (last - 1) / S;
+    const int lead = NB < S ? NB : S;
+    ItemCursor at{first / S, static_cast<int>(first % S)};
+
+    // Current token state: dO (packed), delta and the softmax statistics.
+    u32x4 g[CH];
+    float delta, run_max, inv_sum;
+    TokenRows<CH> pend;  // rows of the next token, between request and fold
+    auto fold = [&]() __attribute__((always_inline)) {
+      if constexpr (!NOMASK) mask_range<G, CH>(lane, D, pend.g);
+      float red[1] = {token_delta<CH>(pend)};
+      group_sum<G, 1>(red, xred, phase);
+      delta = red[0];
+#pragma unroll
+      for (int c = 0; c < CH; ++c) g[c] = pend.g[c];
+      run_max = pend.run_max;
+      inv_sum = pend.inv_sum;
+    };
+    load_token<G, CH, VEC>(a, at.token, lane, pend);
+    fold();
+    __builtin_amdgcn_sched_barrier(0);
+    // The second token's request point may lie before the range start.
+    if (at.source > S - lead && at.token < last_token) load_token<G, CH, VEC>(a, at.token + 1, lane, pend);
+
+    const uint16_t* idle = a.src.row(0, at.token);
+    ItemCursor ahead = at;
+    int64_t ahead_item = first;
+    u32x4 ring[NB][CH];
+    float ring_z[NB];
+    float ring_r[NB];
+    auto refill_slot = [&](int j) __attribute__((always_inline)) {
+      const bool live = ahead_item < last;
+      refill<G, CH, VEC>(a.src, ahead, live, idle, lane, D, ring[j]);
+      const int64_t at_item = live ? ahead.token * S + ahead.source : 0;
+      ring_z[j] = a.logit[at_item];
+      ring_r[j] = a.inv_rms[at_item];
+      if (live) {
+        ++ahead_item;
+        ahead.advance(S);
+      }
+    };
+#pragma unroll
+    for (int j = 0; j < NB; ++j) refill_slot(j);
+
+    auto step = [&](int j, bool refill) __attribute__((always_inline)) {
+      const int s = at.source;
+      const int64_t token = at.token;
+      float dw[1] = {0.0f};
+      {
+        float dw1 = 0.0f;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+          dw[0] = dot2(ring[j][c].x, g[c].x, dw[0]);
+          dw1 = dot2(ring[j][c].y, g[c].y, dw1);
+          dw[0] = dot2(ring[j][c].z, g[c].z, dw[0]);
+          dw1 = dot2(ring[j][c].w, g[c].w, dw1);
+        }
+        dw[0] += dw1;
+      }
+      group_sum<G, 1>(dw, xred, phase);
+      const float z = ring_z[j];
+      const float inv_rms = ring_r[j];
+      const float p = __expf(z - run_max) * inv_sum;
+      const float dz = p * (dw[0] - delta);
+      const float ca = inv_rms * (dz * scale);                  // on q; dq += ca * key
+      const float cb = -(inv_rms * inv_rms) * (dz * z * inv_R);  // on the key coordinates
+      uint16_t* grad_row = a.grad.row(s, token, D);
+      // dO is unpacked per item with a shift and mask the compiler cannot
+      // prove loop-invariant (s >= 0, so both equal the constants): a hoisted
+      // unpacked copy of dO would cost 32 registers per lane.
+      const uint32_t lo_shift = 16u | (static_cast<uint32_t>(s) >> 31);
+      const uint32_t hi_mask = 0xffff0000u | (static_cast<uint32_t>(s) >> 31);
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const int d0 = chunk_start<G>(c, lane);
+        const uint32_t w[4] = {ring[j][c].x, ring[j][c].y, ring[j][c].z, ring[j][c].w};
+        const uint32_t gw[4] = {g[c].x, g[c].y, g[c].z, g[c].w};
+        const float4 qa = *reinterpret_cast<const float4*>(&q_lds[d0]);
+        const float4 qb = *reinterpret_cast<const float4*>(&q_lds[d0 + 4]);
+        const float qf[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+        uint32_t out[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t kw = NOMASK ? w[k] : (w[k] & km[c][k]);
+          const float k0 = bf16_lo(kw), k1 = bf16_hi(kw);
+          const float g0 = __uint_as_float(gw[k] << lo_shift), g1 = __uint_as_float(gw[k] & hi_mask);
+          const float v0 = fmaf(cb, k0, fmaf(ca, qf[2 * k], p * g0));
+          const float v1 = fmaf(cb, k1, fmaf(ca, qf[2 * k + 1], p * g1));
+          dq[c][2 * k] = fmaf(ca, k0, dq[c][2 * k]);
+          dq[c][2 * k + 1] = fmaf(ca, k1, dq[c][2 * k + 1]);
+          out[k] = pack_bf16x2(v0, v1);
+        }
+        if (NOMASK || d0 < D) store_chunk<VEC>(grad_row, d0, D, u32x4{out[0], out[1], out[2], out[3]});
+      }
+
+      if (refill) {
+        __builtin_amdgcn_sched_barrier(0);  // refill the slot after its last use
+        refill_slot(j);
+      }
+      if (token < last_token) {
+        if (s == S - lead) load_token<G, CH, VEC>(a, token + 1, lane, pend);
+        if (s == S - 1) fold();
+      }
+      at.advance(S);
+    };
+
+    // Full rounds refill every slot; the remainder only drains the ring (see
+    // the forward kernel for why no exit test sits between slots).
+    const int64_t items = last - first;
+    const int64_t rounds = items / NB;
+    const int rem = static_cast<int>(items - rounds * NB);
+    for (int64_t r = 0; r < rounds; ++r) {
+#pragma unroll
+      for (int j = 0; j < NB; ++j) step(j, true);
+    }
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      if (j < rem) step(j, false);
+    }
+  }
+
+  // Fixed-order reduction of the groups' dq into this block's partial row.
+  float* partial = a.partial + static_cast<int64_t>(blockIdx.x) * R;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) dq_lds[group * (G * kVec) + lane * kVec + e] = dq[c][e];
+    __syncthreads();
+    for (int j = threadIdx.x; j < G * kVec; j += kBlock) {
+      float t = dq_lds[j];
+#pragma unroll
+      for (int k = 1; k < kGroups; ++k) t += dq_lds[k * (G * kVec) + j];
+      const int d = c * G * kVec + j;
+      if (d >= tail0 && d < D) partial[d - tail0] = t;
+    }
+    __syncthreads();
+  }
+}
+
+// ----------------------------------------------------------------- launchers
+
+// Ring depth (rows in flight per group) for a chunk count.  Measured on
+// MI355X at S=25, D=2048: the forward is equally fast with 3 or 4 rows in
+// flight (2 is slower); the backward is fastest with one row per group,
+// because every further slot costs occupancy.
+template <int CH>
+constexpr int fwd_ring() { return CH <= 4 ? 4 : 2; }
+template <int CH>
+constexpr int bwd_ring() { return 1; }
+
+// Workgroups of `kernel` resident on the current device (cached per kernel
+// and device; 0 if the runtime cannot tell).
+template <class Kernel>
+int64_t resident_blocks(Kernel kernel) {
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return 0;
+  static thread_local int cached_device = -1;
+  static thread_local int64_t cached = 0;
+  if (cached_device == device) return cached;
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kernel), kBlock, 0) !=
+          hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  cached_device = device;
+  cached = static_cast<int64_t>(cus) * per_cu;
+  return cached;
+}
+
+// One token per group: workgroups that start as others retire spread the
+// output stores over time (a persistent grid, whose groups all finish a token
+// at once, measured 5% slower).
+template <int G, int CH, bool NOMASK, bool VEC, class Rows>
+void launch_fwd(const FwdArgs<Rows>& a, hipStream_t stream) {
+  constexpr int64_t kGroups = kBlock / G;
+  const int64_t blocks = (a.n_tokens + kGroups - 1) / kGroups;
+  hipLaunchKernelGGL((attnres_fwd_kernel<G, CH, fwd_ring<CH>(), NOMASK, VEC, Rows>),
+                     dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream, a);
+}
+
+template <int G, int CH, class Rows>
+void launch_fwd_geometry(const FwdArgs<Rows>& a, bool nomask, bool vec, hipStream_t stream) {
+  if (nomask) {
+    if (vec) launch_fwd<G, CH, true, true>(a, stream);
+    else launch_fwd<G, CH, true, false>(a, stream);
+  } else {
+    if (vec) launch_fwd<G, CH, false, true>(a, stream);
+    else launch_fwd<G, CH, false, false>(a, stream);
+  }
+}
+
+template <int G, int CH, bool NOMASK, bool VEC, class Rows, class Grads>
+int64_t launch_bwd(const BwdArgs<Rows, Grads>& a, hipStream_t stream) {
+  const int64_t resident =
+      resident_blocks(&attnres_bwd_kernel<G, CH, bwd_ring<CH>(), NOMASK, VEC, Rows, Grads>);
+  const int64_t blocks = grid_blocks(a.n_tokens, a.width, resident);
+  hipLaunchKernelGGL((attnres_bwd_kernel<G, CH, bwd_ring<CH>(), NOMASK, VEC, Rows, Grads>),
+                     dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream, a);
+  return blocks;
+}
+
+template <int G, int CH, class Rows, class Grads>
+int64_t launch_bwd_geometry(const BwdArgs<Rows, Grads>& a, bool nomask, bool vec, hipStream_t stream) {
+  if (nomask) return vec ? launch_bwd<G, CH, true, true>(a, stream) : launch_bwd<G, CH, true, false>(a, stream);
+  return vec ? launch_bwd<G, CH, false, true>(a, stream) : launch_bwd<G, CH, false, false>(a, stream);
+}
+
+#if defined(ATTNRES_LANES) && defined(ATTNRES_CHUNKS)
+template void launch_fwd_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, PackedRows>(const FwdArgs<PackedRows>&, bool,
+                                                                             bool, hipStream_t);
+template void launch_fwd_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, ListRows>(const FwdArgs<ListRows>&, bool, bool,
+                                                                           hipStream_t);
+template int64_t launch_bwd_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, PackedRows, PackedGrads>(
+    const BwdArgs<PackedRows, PackedGrads>&, bool, bool, hipStream_t);
+template int64_t launch_bwd_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, ListRows, ListGrads>(
+    const BwdArgs<ListRows, ListGrads>&, bool, bool, hipStream_t);
+#else
+#error "compile attnres_kernels.hip with -DATTNRES_LANES=<G> -DATTNRES_CHUNKS=<CH>"
+#endif
+
+}  // namespace attnres_hip
