@@ -1,0 +1,203 @@
+"""Public API behaviour on CPU: signature, validation order, error classes
+and message substrings, container handling and the ops' fake kernels.
+
+Mirrors the reference's tests/test_api.py (CPU part) and the fake-kernel
+checks of tests/test_softmax_stats.py:18-25 and
+tests/test_fla_production_autotune.py:65-130.  No GPU and no kernel launch:
+device rejection happens before the native library is loaded.
+"""
+
+from __future__ import annotations
+
+import inspect
+import sys
+
+import pytest
+import torch
+
+import attnres as package
+from attnres import LearnedQuery, attnres
+
+
+def test_public_surface():
+    assert set(package.__all__) == {"attnres", "LearnedQuery", "__version__"}
+    parameters = inspect.signature(attnres).parameters
+    assert list(parameters) == ["values", "query", "eps", "scale"]
+    assert parameters["eps"].kind is inspect.Parameter.KEYWORD_ONLY
+    assert parameters["eps"].default == 2**-23
+    assert parameters["scale"].default == 1.0
+    assert "keys" not in parameters
+    with pytest.raises(TypeError, match="keys"):
+        attnres(torch.randn(3, 8, dtype=torch.bfloat16), torch.randn(2, dtype=torch.bfloat16),
+                keys=torch.randn(3, 2))
+
+
+@pytest.mark.parametrize("container", [list, tuple])
+def test_cpu_source_list_is_rejected_without_loading_the_native_library(container, monkeypatch):
+    for name in [n for n in sys.modules if n.startswith("attnres._ops")]:
+        monkeypatch.delitem(sys.modules, name)
+    from attnres import _native
+    monkeypatch.setattr(_native, "_library", None)
+    values = container(torch.randn(2, 8, dtype=torch.bfloat16, requires_grad=True) for _ in range(3))
+    query = torch.randn(4, dtype=torch.bfloat16, requires_grad=True)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        attnres(values, query)
+    assert _native._library is None
+
+
+def test_cpu_packed_and_fp32_inputs_are_rejected_explicitly():
+    values = torch.randn(5, 2, 13, dtype=torch.bfloat16)
+    query = torch.randn(4, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        attnres(values, query)
+    with pytest.raises(TypeError, match="BF16"):
+        attnres(values.float(), query)
+    with pytest.raises(TypeError, match="BF16"):
+        attnres(values, query.float())
+
+
+def test_numeric_options_are_validated_before_the_device():
+    values = torch.randn(4, 3, 9, dtype=torch.bfloat16)
+    query = torch.randn(3, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="eps"):
+        attnres(values, query, eps=0.0)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        attnres(values, query, eps=2**-20, scale=0.75)
+
+
+@pytest.mark.parametrize("values,query,error", [
+    (torch.randn(4), torch.randn(2), ValueError),
+    (torch.randn(4, 8, dtype=torch.bfloat16), torch.randn(2, 1, dtype=torch.bfloat16), ValueError),
+    (torch.randn(4, 8, dtype=torch.float16), torch.randn(2), TypeError),
+    (torch.randn(4, 8, dtype=torch.bfloat16), torch.randn(2, dtype=torch.float16), TypeError),
+    (torch.randn(130, 8, dtype=torch.bfloat16), torch.randn(2, dtype=torch.bfloat16), ValueError),
+    (torch.randn(3, 8193, dtype=torch.bfloat16), torch.randn(2, dtype=torch.bfloat16), ValueError),
+    (torch.randn(3, 8, dtype=torch.bfloat16), torch.randn(9, dtype=torch.bfloat16), ValueError),
+    (torch.randn(3, 0, 8, dtype=torch.bfloat16), torch.randn(2, dtype=torch.bfloat16), ValueError),
+])
+def test_packed_rejects_invalid_shapes_and_storage(values, query, error):
+    with pytest.raises(error):
+        attnres(values, query)
+
+
+@pytest.mark.parametrize("kwargs", [{"eps": 0.0}, {"eps": -1.0}, {"eps": float("nan")},
+                                    {"scale": float("inf")}, {"scale": float("nan")}])
+@pytest.mark.parametrize("sequence", [False, True])
+def test_invalid_numeric_options(kwargs, sequence):
+    values = torch.randn(3, 8, dtype=torch.bfloat16)
+    query = torch.randn(4, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        attnres(list(values.unbind(0)) if sequence else values, query, **kwargs)
+
+
+@pytest.mark.parametrize("values,query,error", [
+    ([], torch.randn(2, dtype=torch.bfloat16), ValueError),
+    ([torch.randn(2, 5, dtype=torch.bfloat16), torch.randn(3, 5, dtype=torch.bfloat16)],
+     torch.randn(2, dtype=torch.bfloat16), ValueError),
+    ([torch.randn(2, 5, dtype=torch.bfloat16), 3], torch.randn(2, dtype=torch.bfloat16), TypeError),
+    ([torch.randn(2, 5, dtype=torch.bfloat16)], torch.randn(6, dtype=torch.bfloat16), ValueError),
+    ({"source": torch.randn(2, 5, dtype=torch.bfloat16)}, torch.randn(2, dtype=torch.bfloat16), TypeError),
+    ([torch.randn(2, 5, dtype=torch.bfloat16)], torch.randn(2, device="meta", dtype=torch.bfloat16), TypeError),
+    ([torch.randn(2, 5, dtype=torch.bfloat16)] * 130, torch.randn(2, dtype=torch.bfloat16), ValueError),
+    ([torch.randn(2, 5, dtype=torch.bfloat16), torch.randn(2, 5)], torch.randn(2, dtype=torch.bfloat16), TypeError),
+    ([torch.randn(2, 5)], torch.randn(2, dtype=torch.bfloat16), TypeError),
+    ([torch.randn((), dtype=torch.bfloat16)], torch.randn(1, dtype=torch.bfloat16), ValueError),
+])
+def test_source_containers_reject_malformed_inputs(values, query, error):
+    with pytest.raises(error):
+        attnres(values, query)
+
+
+@pytest.mark.parametrize("container", [None, list, tuple])
+@pytest.mark.parametrize("query", [None, 2, [1.0, 2.0]])
+def test_query_type_errors_are_consistent_across_containers(container, query):
+    values = torch.randn(3, 8, dtype=torch.bfloat16)
+    with pytest.raises(TypeError, match="query"):
+        attnres(container(values.unbind(0)) if container else values, query)
+
+
+@pytest.mark.parametrize("container", [None, list, tuple])
+@pytest.mark.parametrize("name", ["eps", "scale"])
+@pytest.mark.parametrize("value", [True, "0.5", torch.tensor(0.5)])
+def test_scalar_type_errors_are_consistent_across_containers(container, name, value):
+    values = torch.randn(3, 8, dtype=torch.bfloat16)
+    query = torch.randn(2, dtype=torch.bfloat16)
+    with pytest.raises(TypeError):
+        attnres(container(values.unbind(0)) if container else values, query, **{name: value})
+
+
+@pytest.mark.parametrize("container", [None, list, tuple])
+def test_real_integer_and_numpy_scalars_are_accepted(container):
+    np = pytest.importorskip("numpy")
+    values = torch.randn(3, 8, dtype=torch.bfloat16)
+    query = torch.randn(2, dtype=torch.bfloat16)
+    source = container(values.unbind(0)) if container else values
+    for eps, scale in ((1, 2), (np.float32(1e-3), np.int64(3))):
+        with pytest.raises(RuntimeError, match="CUDA"):  # validation passed; only the device fails
+            attnres(source, query, eps=eps, scale=scale)
+
+
+def test_learned_query_parameter():
+    torch.manual_seed(0)
+    module = LearnedQuery(96, init_std=0.02)
+    query = module()
+    assert query.dtype == torch.bfloat16 and query.shape == (96,)
+    assert isinstance(module.query, torch.nn.Parameter)
+    assert 0.005 < float(query.detach().float().std()) < 0.05
+    for bad, error in ((0, ValueError), (True, TypeError), (2.5, TypeError)):
+        with pytest.raises(error):
+            LearnedQuery(bad)
+    with pytest.raises(ValueError):
+        LearnedQuery(4, init_std=0.0)
+
+
+# ---------------------------------------------------------------- fake ops
+
+def _ops():
+    from attnres import _ops
+    return _ops
+
+
+def test_packed_fake_kernels_give_shapes_and_dtypes():
+    ops = _ops()
+    values = torch.empty(5, 7, 48, dtype=torch.bfloat16, device="meta")
+    query = torch.empty(16, dtype=torch.bfloat16, device="meta")
+    out, refine, logit, inv_rms, stats = ops.packed_forward(values, query, 2**-23, 1.0)
+    assert out.shape == (7, 48) and out.dtype == torch.bfloat16
+    assert refine.shape == (7, 48) and refine.dtype == torch.int8
+    assert logit.shape == inv_rms.shape == (7, 5) and logit.dtype == torch.float32
+    assert stats.shape == (2, 7) and stats.dtype == torch.float32
+    grad_values, grad_query = ops.packed_backward(values, query, out, refine, out, logit, inv_rms,
+                                                  stats, 1.0)
+    assert grad_values.shape == values.shape and grad_values.dtype == torch.bfloat16
+    assert grad_query.shape == query.shape and grad_query.dtype == torch.bfloat16
+
+
+@pytest.mark.parametrize("count", [1, 2, 4, 9])
+def test_source_fake_kernels_give_one_gradient_per_position(count):
+    ops = _ops()
+    sources = [torch.empty(2, 3, 64, dtype=torch.bfloat16, device="meta")] * count
+    query = torch.empty(16, dtype=torch.bfloat16, device="meta")
+    out, refine, logit, inv_rms, stats = ops.sources_forward(sources, query, 2**-23, 1.0)
+    assert out.shape == (2, 3, 64) and refine.shape == (6, 64)
+    assert logit.shape == (6, count) and stats.shape == (2, 6) and stats.dtype == torch.float32
+    grads = ops.sources_backward(sources, query, out, refine, out, logit, inv_rms, stats, 1.0)
+    assert len(grads) == count + 1
+    assert all(g.shape == (2, 3, 64) for g in grads[:count]) and grads[count].shape == (16,)
+
+
+def test_row_layout_flattening():
+    """Rows of [..., D] flatten to one row stride when the batch axes are
+    affine (size-1 axes are free), else the tensor is copied (reference
+    src/attnres/_kernels/fla_full_sources.py:164-178)."""
+    ops = _ops()
+    base = torch.empty(4, 6, 10)
+    assert ops.row_stride(base) == 10
+    assert ops.row_stride(base[:, :, :7]) == 10          # padded rows stay addressable
+    assert ops.row_stride(base.transpose(0, 1)) is None   # batch axes out of order
+    assert ops.row_stride(base[..., ::2]) is None         # features not unit-stride
+    assert ops.row_stride(torch.empty(1, 1, 9)) == 0      # single row
+    single = torch.empty(8, 1, 5).as_strided((8, 1, 5), (5, 999, 1))
+    assert ops.row_stride(single) == 5
+    tensor, stride = ops.prepare_rows(base.transpose(0, 1))
+    assert tensor.is_contiguous() and stride == 10
