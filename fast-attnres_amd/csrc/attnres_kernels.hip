@@ -25,9 +25,9 @@
 // of the full row) is updated; the per-source logit and 1/rms and the
 // per-token (max, 1/sum) are saved for the backward.
 //
-// Backward.  The N*S (token, source) items are split into equal contiguous
-// ranges, one per group of a persistent grid, so every group streams the
-// same number of rows.  The ring of value rows crosses token boundaries;
+// Backward.  A persistent grid; group g takes tokens g, g + groups, ... so
+// that the groups work on neighbouring tokens at any time and walk the
+// sources roughly in step.  The ring of value rows crosses token boundaries;
 // at each new token the group loads dO and the saved output (BF16 plus one
 // refinement byte per element, see refine_encode) and forms
 // delta = <dO, o>.  Per item: dw = <v, dO>, p = exp(z - max) / sum,
@@ -301,22 +301,15 @@ __device__ __forceinline__ int group_index() {
   }
 }
 
-// Contiguous share [first, last) of `count` work units for group `gid` of
-// `groups` (shares differ in size by at most one unit).
-__device__ __forceinline__ void share(int64_t count, int64_t gid, int64_t groups, int64_t& first,
-                                      int64_t& last) {
-  first = gid * count / groups;
-  last = (gid + 1) * count / groups;
-}
-
-// Cursor over (token, source) items in token-major order.
+// Cursor over a group's (token, source) items in token-major order.
 struct ItemCursor {
   int64_t token;
   int source;
+  int64_t stride = 1;  // tokens between a group's consecutive tokens
   __device__ __forceinline__ void advance(int S) {
     if (++source == S) {
       source = 0;
-      ++token;
+      token += stride;
     }
   }
 };
@@ -344,8 +337,9 @@ __device__ __forceinline__ void refill(const Rows& src, const ItemCursor& at, bo
 // NOMASK: R == D and D == G*CH*8, so every lane position is an in-range key
 // coordinate and no word masks are needed.
 //
-// Persistent: each group owns a contiguous range of tokens and streams their
-// S*tokens rows through the ring without draining it between tokens.
+// Group g takes tokens g, g + groups, ... and streams their rows through the
+// ring without draining it between tokens (launched with one token per group,
+// see launch_fwd).
 template <int G, int CH, int NB, bool NOMASK, bool VEC, class Rows>
 __global__ void __launch_bounds__(kBlock) attnres_fwd_kernel(const FwdArgs<Rows> a) {
   static_assert(G <= 64 || G == kBlock, "a wide group is the whole workgroup");
@@ -359,20 +353,23 @@ __global__ void __launch_bounds__(kBlock) attnres_fwd_kernel(const FwdArgs<Rows>
   const float inv_R = 1.0f / static_cast<float>(a.rank);
   int phase = 0;
 
-  int64_t t_first, t_last;
-  share(a.n_tokens, static_cast<int64_t>(blockIdx.x) * kGroups + group,
-        static_cast<int64_t>(gridDim.x) * kGroups, t_first, t_last);
-  if (t_first >= t_last) return;  // whole group idle (no barrier follows for it)
+  // Group gid takes tokens gid, gid + groups, ... (see the backward kernel);
+  // items are counted per group: item i is source i % S of the group's
+  // token i / S.
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * kGroups + group;
+  const int64_t groups = static_cast<int64_t>(gridDim.x) * kGroups;
+  const int64_t my_tokens = gid < a.n_tokens ? (a.n_tokens - 1 - gid) / groups + 1 : 0;
+  if (my_tokens == 0) return;  // whole group idle (no barrier follows for it)
 
   uint32_t qw[CH][4];
   load_query_words<G, CH>(a.query, lane, D, tail0, qw);
   uint32_t km[CH][4];
   if constexpr (!NOMASK) key_masks<G, CH>(lane, D, tail0, km);
 
-  const int64_t last = t_last * S;
-  const uint16_t* idle = a.src.row(0, t_first);
-  ItemCursor ahead{t_first, 0};
-  int64_t ahead_item = t_first * S;
+  const int64_t last = my_tokens * S;
+  const uint16_t* idle = a.src.row(0, gid);
+  ItemCursor ahead{gid, 0, groups};
+  int64_t ahead_item = 0;
   u32x4 ring[NB][CH];
 #pragma unroll
   for (int j = 0; j < NB; ++j) {
@@ -393,7 +390,7 @@ __global__ void __launch_bounds__(kBlock) attnres_fwd_kernel(const FwdArgs<Rows>
     for (int e = 0; e < kVec; ++e) acc[c][e] = 0.0f;
   float run_max = -INFINITY;
   float run_sum = 0.0f;
-  ItemCursor at{t_first, 0};
+  ItemCursor at{gid, 0, groups};
 
   // One item: the row in ring slot j.  `refill_slot` is false only in the
   // remainder after the last full round, where every row is already loaded.
@@ -489,7 +486,7 @@ __global__ void __launch_bounds__(kBlock) attnres_fwd_kernel(const FwdArgs<Rows>
   // Full rounds refill every slot (with an idle load past the end), so the
   // loop body has no exit test between slots: any such path back to the loop
   // head would make the compiler wait there for all outstanding loads.
-  const int64_t items = last - t_first * S;
+  const int64_t items = last;
   const int64_t rounds = items / NB;
   const int rem = static_cast<int>(items - rounds * NB);
   for (int64_t r = 0; r < rounds; ++r) {
@@ -582,9 +579,9 @@ __device__ __forceinline__ float token_delta(const TokenRows<CH>& t) {
   return (m0 + m1) + corr;
 }
 
-// Persistent: the N*S items are split into equal contiguous ranges, one per
-// group, and the value rows stream through the ring across token
-// boundaries.  The next token's dO, output, refinement bytes and statistics
+// Persistent: group g takes tokens g, g + groups, ..., and the value rows
+// stream through the ring across token boundaries.  The next token's dO,
+// output, refinement bytes and statistics
 // are requested `lead` = min(NB, S) items before the current token ends,
 // right after a ring refill, and folded into delta on the token's last item
 // -- when the younger rows in the ring are still in flight -- so a token
@@ -621,14 +618,21 @@ __global__ void __launch_bounds__(kBlock) attnres_bwd_kernel(const BwdArgs<Rows,
 #pragma unroll
     for (int e = 0; e < kVec; ++e) dq[c][e] = 0.0f;
 
-  int64_t first, last;
-  share(a.n_tokens * S, static_cast<int64_t>(blockIdx.x) * kGroups + group,
-        static_cast<int64_t>(gridDim.x) * kGroups, first, last);
+  // Group gid takes tokens gid, gid + groups, ...: at any time the groups
+  // work on neighbouring tokens and walk the sources roughly in step, so the
+  // rows in flight on the device lie in few, compact address ranges (row
+  // blocks spread over the whole buffer are read and written measurably
+  // slower).  Items are counted per group: first = 0, last = tokens * S.
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * kGroups + group;
+  const int64_t groups = static_cast<int64_t>(gridDim.x) * kGroups;
+  const int64_t my_tokens = gid < a.n_tokens ? (a.n_tokens - 1 - gid) / groups + 1 : 0;
+  const int64_t first = 0;
+  const int64_t last = my_tokens * S;
 
   if (first < last) {
-    const int64_t last_token = (last - 1) / S;
+    const int64_t last_token = gid + (my_tokens - 1) * groups;
     const int lead = NB < S ? NB : S;
-    ItemCursor at{first / S, static_cast<int>(first % S)};
+    ItemCursor at{gid, 0, groups};
 
     // Current token state: dO (packed), delta and the softmax statistics.
     u32x4 g[CH];
@@ -648,7 +652,7 @@ __global__ void __launch_bounds__(kBlock) attnres_bwd_kernel(const BwdArgs<Rows,
     fold();
     __builtin_amdgcn_sched_barrier(0);
     // The second token's request point may lie before the range start.
-    if (at.source > S - lead && at.token < last_token) load_token<G, CH, VEC>(a, at.token + 1, lane, pend);
+    if (at.source > S - lead && at.token < last_token) load_token<G, CH, VEC>(a, at.token + groups, lane, pend);
 
     const uint16_t* idle = a.src.row(0, at.token);
     ItemCursor ahead = at;
@@ -726,7 +730,7 @@ __global__ void __launch_bounds__(kBlock) attnres_bwd_kernel(const BwdArgs<Rows,
         refill_slot(j);
       }
       if (token < last_token) {
-        if (s == S - lead) load_token<G, CH, VEC>(a, token + 1, lane, pend);
+        if (s == S - lead) load_token<G, CH, VEC>(a, token + groups, lane, pend);
         if (s == S - 1) fold();
       }
       at.advance(S);
