@@ -1,6 +1,6 @@
 """Benchmark of one Fast-AttnRes read (forward + backward) on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2|c3|c4|c5]
 
 A "step" is one read: ``out = attnres(values, query)`` followed by
 ``torch.autograd.grad(out, (values, query), dO)``, the public path with the
@@ -24,6 +24,17 @@ timed with HIP events recorded on the stream the kernels run on; its
 (profiles/attnres_<config>_hbm_traffic.json).  ``cpu_baseline`` times the CPU
 FP32 oracle (test infrastructure under ``oracle/``) on the host over a
 bounded sample of the same inputs.
+
+Other configurations (not the headline line): ``c3`` is the sliced
+low-rank packed read [S=16, N=16384, D=4096], R=1024.  ``c4`` is the Block
+schedule with list input: 9 separately allocated [N=32768, D=2048] sources
+(8 block sums, std sqrt(3)*U[0.5, 2]; 1 embedding, std 1) shared by 3 reads
+with their own queries; a step is the 3 reads forward and backward, and the
+gradient accumulation over the reads (what autograd adds for shared
+sources) is timed separately from the operator.  ``c5`` is the 24-layer
+Full-schedule sweep: one packed read for each S = 1..48 at N=16384, for
+D in {1024, 4096} and R in {D, D/4}; a step is the 48 reads of one (D, R)
+and the line reports the summed operator time per step.
 
 ``--copy-probe`` runs only a plain device copy of known size, used to scale
 the hardware FETCH_SIZE / WRITE_SIZE counters when profiling.
@@ -53,6 +64,10 @@ CONFIGS = {
                name="standard-full-read S=25 N=16384 D=2048 R=2048 packed"),
     "c3": dict(sources=16, batch=(16384,), width=4096, rank=1024,
                name="sliced-lowrank-read S=16 N=16384 D=4096 R=1024 packed"),
+    "c4": dict(sources=9, batch=(32768,), width=2048, rank=2048, reads=3,
+               name="block-schedule list S=9 N=32768 D=2048 R=2048, 3 reads sharing the sources"),
+    "c5": dict(sources=48, batch=(16384,), widths=(1024, 4096),
+               name="24-layer full-schedule sweep S=1..48 N=16384 D in {1024,4096} R in {D,D/4} packed"),
 }
 
 
@@ -146,6 +161,140 @@ def cpu_baseline(values, query, grad_out, budget_s: float, chunk: int) -> dict:
     }
 
 
+def _event():
+    import torch
+
+    return torch.cuda.Event(enable_timing=True)
+
+
+def run_block_schedule(cfg: dict, steps: int, warmup: int) -> dict:
+    """c4: 3 reads of one ordered list of 9 sources, each read with its own
+    query; per read forward, then per read backward (so the operator time
+    excludes the gradient accumulation over the shared sources, which is
+    timed on its own, as autograd's adds)."""
+    import torch
+
+    from attnres import attnres
+
+    device = torch.device("cuda:0")
+    generator = torch.Generator(device=device).manual_seed(0)
+    tokens, width, rank, reads = cfg["batch"][0], cfg["width"], cfg["rank"], cfg["reads"]
+    sources = []
+    for s in range(cfg["sources"]):  # source 0: embedding (std 1); then block sums
+        std = 1.0 if s == 0 else math.sqrt(3.0) * (0.5 + 1.5 * float(torch.rand((), generator=generator, device=device)))
+        noise = torch.randn(tokens, width, generator=generator, device=device)
+        sources.append((noise * std).to(torch.bfloat16).requires_grad_())
+    queries = [(torch.randn(rank, generator=generator, device=device) / math.sqrt(rank)).to(torch.bfloat16).requires_grad_()
+               for _ in range(reads)]
+    grad_outs = [torch.randn(tokens, width, generator=generator, device=device).to(torch.bfloat16) for _ in range(reads)]
+    listed = tuple(sources)
+
+    def step(ev=None):
+        if ev: ev[0].record()
+        outs = [attnres(listed, queries[k]) for k in range(reads)]
+        if ev: ev[1].record()
+        per_read = [torch.autograd.grad(outs[k], (*listed, queries[k]), grad_outs[k]) for k in range(reads)]
+        if ev: ev[2].record()
+        total = [sum(g[i] for g in per_read[1:]) + per_read[0][i] for i in range(len(listed))]
+        if ev: ev[3].record()
+        return total
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    events = [[_event() for _ in range(4)] for _ in range(steps)]
+    for i in range(steps):
+        step(events[i])
+    torch.cuda.synchronize()
+    fwd_ms = statistics.fmean(e[0].elapsed_time(e[1]) for e in events)
+    bwd_ms = statistics.fmean(e[1].elapsed_time(e[2]) for e in events)
+    acc_ms = statistics.fmean(e[2].elapsed_time(e[3]) for e in events)
+    fwd_bytes, bwd_bytes = read_bytes(cfg["sources"], tokens, width)
+    op_ms = fwd_ms + bwd_ms
+    value = reads * (fwd_bytes + bwd_bytes) / (op_ms * 1e-3) / 1e12
+    fwd_tbs = reads * fwd_bytes / (fwd_ms * 1e-3) / 1e12
+    bwd_tbs = reads * bwd_bytes / (bwd_ms * 1e-3) / 1e12
+    return {
+        "metric": "c4 block schedule (list input): operator fwd+bwd time per 3 reads and achieved HBM TB/s",
+        "value": round(value, 4), "unit": "TB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(op_ms, 5), "us_per_read": round(op_ms * 1e3 / reads, 2),
+        "pct_of_peak": round(100 * value / HBM_PEAK_TBS, 2), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "storage_dtype": "bf16",
+        "data": "synthetic (seeded; embedding std 1, block sums std sqrt(3)*U[0.5,2])",
+        "config": {"workload": cfg["name"], "sources": cfg["sources"], "tokens": tokens, "width": width,
+                   "rank": rank, "layout": "list", "reads_per_step": reads,
+                   "bytes_per_read": fwd_bytes + bwd_bytes},
+        "forward": {"us_per_read": round(fwd_ms * 1e3 / reads, 2), "TB/s": round(fwd_tbs, 4)},
+        "backward": {"us_per_read": round(bwd_ms * 1e3 / reads, 2), "TB/s": round(bwd_tbs, 4)},
+        "gradient_accumulation": {"us_per_step": round(acc_ms * 1e3, 2),
+                                  "what": "adds of the 3 reads' source gradients (outside the operator)"},
+        "roofline": {"bound": "hbm", "kernel": "backward op (list layout)", "achieved": round(bwd_tbs * 1e3, 1),
+                     "peak": HBM_PEAK_TBS * 1e3, "unit": "GB/s", "frac": round(bwd_tbs / HBM_PEAK_TBS, 4),
+                     "traffic": measured_traffic("c4", "backward_bytes")},
+        "cpu_baseline": None,
+    }
+
+
+def run_sweep(cfg: dict, steps: int, warmup: int) -> dict:
+    """c5: one packed read per S = 1..48 (N=16384) for each D and R in
+    {D, D/4}; the value rows of a read are the first S sources of one
+    [48, N, D] tensor (a view, no copy)."""
+    import torch
+
+    from attnres import attnres
+
+    device = torch.device("cuda:0")
+    tokens = cfg["batch"][0]
+    max_sources = cfg["sources"]
+    total_bytes, total_ms, sweep = 0, 0.0, []
+    for width in cfg["widths"]:
+        for rank in (width, width // 4):
+            values, query, grad_out = make_inputs(dict(sources=max_sources, batch=(tokens,), width=width, rank=rank),
+                                                  device, seed=width + rank)
+            query.requires_grad_(True)
+            per_read, step_ms, step_bytes = [], 0.0, 0
+            for sources in range(1, max_sources + 1):
+                leaf = values[:sources].detach().requires_grad_()
+
+                def read():
+                    out = attnres(leaf, query)
+                    return torch.autograd.grad(out, (leaf, query), grad_out)
+
+                for _ in range(warmup):
+                    read()
+                start, stop = _event(), _event()
+                start.record()
+                for _ in range(steps):
+                    read()
+                stop.record()
+                torch.cuda.synchronize()
+                ms = start.elapsed_time(stop) / steps
+                fwd_bytes, bwd_bytes = read_bytes(sources, tokens, width)
+                per_read.append([sources, round(ms * 1e3, 2), round((fwd_bytes + bwd_bytes) / (ms * 1e-3) / 1e12, 4)])
+                step_ms += ms
+                step_bytes += fwd_bytes + bwd_bytes
+            del values, grad_out
+            torch.cuda.empty_cache()
+            sweep.append({"width": width, "rank": rank, "ms_per_step": round(step_ms, 4),
+                          "TB/s": round(step_bytes / (step_ms * 1e-3) / 1e12, 4),
+                          "bytes_per_step": step_bytes, "per_read_S_us_TBs": per_read})
+            total_bytes += step_bytes
+            total_ms += step_ms
+    value = total_bytes / (total_ms * 1e-3) / 1e12
+    return {
+        "metric": "c5 24-layer full-schedule sweep: summed operator fwd+bwd time per step (48 reads) and TB/s",
+        "value": round(value, 4), "unit": "TB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(total_ms / len(sweep), 4), "higher_is_better": True, "scaling": "weak",
+        "pct_of_peak": round(100 * value / HBM_PEAK_TBS, 2), "vs_baseline": None, "dtype": "f32",
+        "storage_dtype": "bf16", "data": "synthetic (seeded; per-source std U[0.5,4], 1% channels x8)",
+        "config": {"workload": cfg["name"], "tokens": tokens, "layout": "packed",
+                   "note": "ms_per_step is the mean over the four (D, R) steps; each step's own time is in sweep"},
+        "sweep": sweep,
+        "roofline": None,
+        "cpu_baseline": None,
+    }
+
+
 def main(argv=None) -> int:
     parser = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -176,6 +325,11 @@ def main(argv=None) -> int:
 
     _native.load()  # fail loudly if the HIP library is missing
     cfg = CONFIGS[args.config]
+    if args.config in ("c4", "c5"):
+        torch.cuda.set_device(0)
+        run = run_block_schedule if args.config == "c4" else run_sweep
+        print(json.dumps(run(cfg, args.steps, args.warmup)), flush=True)
+        return 0
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
     values, query, grad_out = make_inputs(cfg, device)
@@ -220,7 +374,9 @@ def main(argv=None) -> int:
     fwd_tbs = fwd_bytes / (fwd_avg * 1e-3) / 1e12
 
     record = {
-        "metric": "fwd+bwd us/read and achieved HBM TB/s (% peak), S=25 D=2048 N=16K tokens",
+        "metric": ("fwd+bwd us/read and achieved HBM TB/s (% peak), S=25 D=2048 N=16K tokens"
+                   if args.config == "c2" else
+                   f"{args.config} fwd+bwd us/read and achieved HBM TB/s (% peak)"),
         "value": round(value, 4),
         "unit": "TB/s",
         "n_gpus": 1,

@@ -780,10 +780,11 @@ constexpr int fwd_ring() { return CH <= 4 ? 4 : 2; }
 template <int CH>
 constexpr int bwd_ring() { return 1; }
 
-// Workgroups of `kernel` resident on the current device (cached per kernel
-// and device; 0 if the runtime cannot tell).
-template <class Kernel>
-int64_t resident_blocks(Kernel kernel) {
+// Workgroups of `Kernel` resident on the current device (cached per kernel
+// and device; 0 if the runtime cannot tell).  The kernel is a template
+// argument so that every instantiation has its own cache.
+template <auto Kernel>
+int64_t resident_blocks() {
   int device = 0;
   if (hipGetDevice(&device) != hipSuccess) return 0;
   static thread_local int cached_device = -1;
@@ -791,7 +792,7 @@ int64_t resident_blocks(Kernel kernel) {
   if (cached_device == device) return cached;
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kernel), kBlock, 0) !=
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(Kernel), kBlock, 0) !=
           hipSuccess) {
     (void)hipGetLastError();
     return 0;
@@ -826,7 +827,7 @@ void launch_fwd_geometry(const FwdArgs<Rows>& a, bool nomask, bool vec, hipStrea
 template <int G, int CH, bool NOMASK, bool VEC, class Rows, class Grads>
 int64_t launch_bwd(const BwdArgs<Rows, Grads>& a, hipStream_t stream) {
   const int64_t resident =
-      resident_blocks(&attnres_bwd_kernel<G, CH, bwd_ring<CH>(), NOMASK, VEC, Rows, Grads>);
+      resident_blocks<&attnres_bwd_kernel<G, CH, bwd_ring<CH>(), NOMASK, VEC, Rows, Grads>>();
   const int64_t blocks = grid_blocks(a.n_tokens, a.width, resident);
   hipLaunchKernelGGL((attnres_bwd_kernel<G, CH, bwd_ring<CH>(), NOMASK, VEC, Rows, Grads>),
                      dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream, a);
