@@ -36,26 +36,46 @@ __device__ __forceinline__ uint16_t to_bf16(float x) {
   return static_cast<uint16_t>(__builtin_bit_cast(uint32_t, b) & 0xffffu);
 }
 
+// The dq reduction is latency-bound (a few MB): each thread issues all of its
+// loads at once (clamped, unconditional indices) and then adds the values in
+// the fixed order, skipping the clamped ones with a select, so the sums are
+// exactly the in-order sums.
+constexpr int kRowsPerSlice = (kMaxGridBlocks + kFinalizeSlices - 1) / kFinalizeSlices;
+
 // First stage of the dq reduction: slice p sums partial rows p, p+P, p+2P, ...
+// (rows <= kMaxGridBlocks and P = min(rows, kFinalizeSlices), so a slice has at
+// most kRowsPerSlice rows).
 __global__ void __launch_bounds__(kBlock) attnres_dq_slices_kernel(
     const float* __restrict__ partial, int64_t rows, int R, float* __restrict__ slices) {
   const int col = blockIdx.x * kBlock + threadIdx.x;
   const int p = blockIdx.y;
   const int P = gridDim.y;
   if (col >= R) return;
+  float v[kRowsPerSlice];
+#pragma unroll
+  for (int k = 0; k < kRowsPerSlice; ++k) {
+    const int64_t r = p + static_cast<int64_t>(k) * P;
+    v[k] = partial[(r < rows ? r : p) * R + col];
+  }
   float t = 0.0f;
-  for (int64_t r = p; r < rows; r += P) t += partial[r * R + col];
+#pragma unroll
+  for (int k = 0; k < kRowsPerSlice; ++k) t = p + static_cast<int64_t>(k) * P < rows ? t + v[k] : t;
   slices[static_cast<int64_t>(p) * R + col] = t;
 }
 
-// Second stage: dq[r] = sum of the P slices in order; FP32 total and BF16 copy.
+// Second stage: dq[r] = sum of the P <= kFinalizeSlices slices in order; FP32
+// total and BF16 copy.
 __global__ void __launch_bounds__(kBlock) attnres_dq_finalize_kernel(
     const float* __restrict__ slices, int P, int R, float* __restrict__ dq32,
     uint16_t* __restrict__ dq16) {
   const int col = blockIdx.x * kBlock + threadIdx.x;
   if (col >= R) return;
+  float v[kFinalizeSlices];
+#pragma unroll
+  for (int p = 0; p < kFinalizeSlices; ++p) v[p] = slices[static_cast<int64_t>(p < P ? p : 0) * R + col];
   float t = 0.0f;
-  for (int p = 0; p < P; ++p) t += slices[static_cast<int64_t>(p) * R + col];
+#pragma unroll
+  for (int p = 0; p < kFinalizeSlices; ++p) t = p < P ? t + v[p] : t;
   dq32[col] = t;
   dq16[col] = to_bf16(t);
 }
