@@ -36,6 +36,11 @@ Full-schedule sweep: one packed read for each S = 1..48 at N=16384, for
 D in {1024, 4096} and R in {D, D/4}; a step is the 48 reads of one (D, R)
 and the line reports the summed operator time per step.
 
+``model`` is the caller: one training step (forward, backward, AdamW) of the
+24-layer Full-schedule causal LM of ``benchmarks/model.py`` at D=1024 on
+16x1024 tokens, whose 48 residual reads (S = 2..49) are the HIP operator; the
+rest of the model runs in FP32 PyTorch.
+
 ``--copy-probe`` runs only a plain device copy of known size, used to scale
 the hardware FETCH_SIZE / WRITE_SIZE counters when profiling.
 """
@@ -68,6 +73,8 @@ CONFIGS = {
                name="block-schedule list S=9 N=32768 D=2048 R=2048, 3 reads sharing the sources"),
     "c5": dict(sources=48, batch=(16384,), widths=(1024, 4096),
                name="24-layer full-schedule sweep S=1..48 N=16384 D in {1024,4096} R in {D,D/4} packed"),
+    "model": dict(layers=24, width=1024, heads=16, ffn=2816, batch=16, sequence=1024, vocab=8192,
+                  name="24-layer Full-schedule causal LM training step, D=1024, 16x1024 tokens, FP32 outside the reads"),
 }
 
 
@@ -295,6 +302,48 @@ def run_sweep(cfg: dict, steps: int, warmup: int) -> dict:
     }
 
 
+def run_model(cfg: dict, steps: int, warmup: int) -> dict:
+    """model: training steps of the Full-schedule causal LM (benchmarks/model.py)."""
+    import torch
+
+    from benchmarks.model import TrainingConfig, make_model, training_step
+
+    config = TrainingConfig(**{k: cfg[k] for k in ("layers", "width", "heads", "ffn", "batch", "sequence", "vocab")},
+                            mode="full", source_layout="packed")
+    torch.manual_seed(0)
+    model = make_model(config, backend="kernel").cuda()
+    optimizer = torch.optim.AdamW(model.parameters(), lr=1e-4)
+    generator = torch.Generator(device="cuda").manual_seed(0)
+    tokens = torch.randint(config.vocab, (config.batch, config.sequence), device="cuda", generator=generator)
+    targets = torch.roll(tokens, -1, dims=1)
+    for _ in range(warmup):
+        training_step(model, optimizer, tokens, targets)
+    torch.cuda.synchronize()
+    start, stop = _event(), _event()
+    start.record()
+    for _ in range(steps):
+        loss = training_step(model, optimizer, tokens, targets)
+    stop.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / steps
+    n_tokens = config.batch * config.sequence
+    reads = 2 * config.layers
+    read_bytes_per_step = sum(sum(read_bytes(s, n_tokens, config.width)) for s in range(2, reads + 2))
+    return {
+        "metric": "model: 24-layer Full-schedule causal LM training step (48 AttnRes reads, S=2..49), tokens/s",
+        "value": round(n_tokens / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps,
+        "warmup": warmup, "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32 model, bf16 reads", "data": "synthetic tokens (seeded)",
+        "config": {"workload": cfg["name"], "layers": config.layers, "width": config.width, "heads": config.heads,
+                   "ffn": config.ffn, "batch": config.batch, "sequence": config.sequence, "vocab": config.vocab,
+                   "reads_per_step": reads, "read_sources": f"2..{reads + 1}",
+                   "attnres_algorithmic_bytes_per_step": read_bytes_per_step},
+        "loss": round(float(loss), 4),
+        "roofline": None,
+        "cpu_baseline": None,
+    }
+
+
 def main(argv=None) -> int:
     parser = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -325,9 +374,9 @@ def main(argv=None) -> int:
 
     _native.load()  # fail loudly if the HIP library is missing
     cfg = CONFIGS[args.config]
-    if args.config in ("c4", "c5"):
+    if args.config in ("c4", "c5", "model"):
         torch.cuda.set_device(0)
-        run = run_block_schedule if args.config == "c4" else run_sweep
+        run = {"c4": run_block_schedule, "c5": run_sweep, "model": run_model}[args.config]
         print(json.dumps(run(cfg, args.steps, args.warmup)), flush=True)
         return 0
     device = torch.device("cuda:0")

@@ -1,0 +1,85 @@
+"""The model caller on the GPU: the HIP read inside the residual stream.
+
+The model (FP32 outside the reads, as in the reference's default) is run with
+the HIP operator on the GPU and with the CPU oracle on the same weights; the
+logits and every parameter gradient must agree within a BF16-read tolerance
+(each read rounds its output to BF16 once, as the oracle does, so the models
+differ only by the reads' last-ulp differences carried through the layers).
+The reference qualifies its model path the same way, by loss and gradient
+parity against the oracle-backed model (`tests/test_pre_timing_gate.py:70-113`).
+"""
+
+from __future__ import annotations
+
+import copy
+
+import pytest
+import torch
+
+from benchmarks.model import TrainingConfig, make_model, training_step
+from oracle.oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _config(mode, layout, variant):
+    return TrainingConfig(layers=3, width=64, heads=4, ffn=128, batch=2, sequence=32, vocab=97,
+                          block_count=2, mode=mode, source_layout=layout, variant=variant,
+                          rank=64 if variant == "standard" else 16)
+
+
+def _relative_error(a, b):
+    return float((a - b).abs().max() / b.abs().max().clamp_min(1e-12))
+
+
+@pytest.mark.parametrize("variant", ["standard", "sliced"])
+@pytest.mark.parametrize("layout", ["packed", "list"])
+@pytest.mark.parametrize("mode", ["full", "block"])
+def test_model_matches_oracle_model(mode, layout, variant):
+    config = _config(mode, layout, variant)
+    print(f"model parity mode={mode} layout={layout} variant={variant}", flush=True)
+    torch.manual_seed(11)
+    reference = make_model(config, backend=oracle)
+    candidate = make_model(config, backend="kernel")
+    candidate.load_state_dict(reference.state_dict())
+    candidate.cuda()
+    tokens = torch.randint(config.vocab, (config.batch, config.sequence))
+    expected = reference(tokens)
+    actual = candidate(tokens.cuda())
+    assert _relative_error(actual.cpu(), expected) < 2e-2
+    weight = torch.randn(expected.shape)
+    (expected * weight).sum().backward()
+    (actual * weight.cuda()).sum().backward()
+    for (name, p), q in zip(candidate.named_parameters(), reference.parameters()):
+        assert p.grad is not None, name
+        assert _relative_error(p.grad.cpu(), q.grad) < 5e-2, name
+
+
+@pytest.mark.parametrize("mode", ["full", "block"])
+def test_compiled_model_step_matches_eager(mode):
+    config = _config(mode, "packed", "standard")
+    print(f"compiled model mode={mode}", flush=True)
+    torch.manual_seed(23)
+    eager = make_model(config, backend="kernel").cuda()
+    compiled_model = copy.deepcopy(eager)
+    tokens = torch.randint(config.vocab, (config.batch, config.sequence), device="cuda")
+    compiled = torch.compile(compiled_model, fullgraph=True, backend="aot_eager")
+    a = eager(tokens)
+    b = compiled(tokens)
+    torch.testing.assert_close(b, a, rtol=1e-4, atol=1e-5)
+    a.float().square().mean().backward()
+    b.float().square().mean().backward()
+    for (name, p), q in zip(eager.named_parameters(), compiled_model.parameters()):
+        torch.testing.assert_close(q.grad, p.grad, rtol=1e-3, atol=1e-6, msg=name)
+
+
+def test_training_steps_reduce_the_loss():
+    config = _config("block", "list", "standard")
+    torch.manual_seed(29)
+    model = make_model(config, backend="kernel").cuda()
+    optimizer = torch.optim.AdamW(model.parameters(), lr=3e-3)
+    tokens = torch.randint(config.vocab, (config.batch, config.sequence), device="cuda")
+    targets = torch.roll(tokens, -1, dims=1)
+    losses = [float(training_step(model, optimizer, tokens, targets)) for _ in range(12)]
+    assert all(torch.isfinite(torch.tensor(losses)))
+    assert losses[-1] < losses[0]
