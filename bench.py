@@ -216,6 +216,39 @@ def run_block_schedule(cfg: dict, steps: int, warmup: int) -> dict:
     fwd_ms = statistics.fmean(e[0].elapsed_time(e[1]) for e in events)
     bwd_ms = statistics.fmean(e[1].elapsed_time(e[2]) for e in events)
     acc_ms = statistics.fmean(e[2].elapsed_time(e[3]) for e in events)
+
+    # Whole steps (forward of the 3 reads + one autograd pass over all of them):
+    # autograd summing the shared sources' gradients vs SharedSources summing
+    # them in the backward kernels.
+    from attnres import SharedSources
+
+    inputs = (*listed, *queries)
+
+    def whole(read):
+        outs = [read(k) for k in range(reads)]
+        return torch.autograd.grad(outs, inputs, grad_outs)
+
+    def timed(read):
+        for _ in range(warmup):
+            whole(read)
+        torch.cuda.synchronize()
+        start, stop = _event(), _event()
+        start.record()
+        for _ in range(steps):
+            whole(read)
+        stop.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) / steps
+
+    plain_ms = timed(lambda k: attnres(listed, queries[k]))
+    bank_state = {}
+
+    def bank_read(k):
+        if k == 0:
+            bank_state["bank"] = SharedSources(listed)
+        return bank_state["bank"].read(queries[k])
+
+    shared_ms = timed(bank_read)
     fwd_bytes, bwd_bytes = read_bytes(cfg["sources"], tokens, width)
     op_ms = fwd_ms + bwd_ms
     value = reads * (fwd_bytes + bwd_bytes) / (op_ms * 1e-3) / 1e12
@@ -235,6 +268,10 @@ def run_block_schedule(cfg: dict, steps: int, warmup: int) -> dict:
         "backward": {"us_per_read": round(bwd_ms * 1e3 / reads, 2), "TB/s": round(bwd_tbs, 4)},
         "gradient_accumulation": {"us_per_step": round(acc_ms * 1e3, 2),
                                   "what": "adds of the 3 reads' source gradients (outside the operator)"},
+        "whole_step": {"autograd_sum_ms": round(plain_ms, 4), "shared_sources_ms": round(shared_ms, 4),
+                       "speedup": round(plain_ms / shared_ms, 3),
+                       "what": "forward of the 3 reads + one autograd.grad over them; SharedSources sums "
+                               "the source gradients in the backward kernels"},
         "roofline": {"bound": "hbm", "kernel": "backward op (list layout)", "achieved": round(bwd_tbs * 1e3, 1),
                      "peak": HBM_PEAK_TBS * 1e3, "unit": "GB/s", "frac": round(bwd_tbs / HBM_PEAK_TBS, 4),
                      "traffic": measured_traffic("c4", "backward_bytes")},

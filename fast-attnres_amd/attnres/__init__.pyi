@@ -1,6 +1,7 @@
 from torch import Tensor
 
 from .modules import LearnedQuery as LearnedQuery
+from .shared import SharedSources as SharedSources
 
 __version__: str
 
@@ -14,4 +15,4 @@ def attnres(
 ) -> Tensor: ...
 
 
-__all__ = ["LearnedQuery", "__version__", "attnres"]
+__all__ = ["LearnedQuery", "SharedSources", "__version__", "attnres"]

@@ -127,19 +127,19 @@ int launch_forward(const FwdArgs<Rows>& a, bool vec, hipStream_t stream) {
 }
 
 template <class Rows, class Grads>
-int launch_backward(const BwdArgs<Rows, Grads>& a, bool vec, float* slices, float* dq32, uint16_t* dq16,
+int launch_backward(const BwdArgs<Rows, Grads>& a, bool vec, bool acc, float* slices, float* dq32, uint16_t* dq16,
                     hipStream_t stream) {
   const Geometry geo = geometry(a.width);
   const bool nomask = no_mask(geo, a.width, a.rank);
   int64_t blocks = 0;
   switch (geo.lanes * 100 + geo.chunks) {
-    case 1601: blocks = launch_bwd_geometry<16, 1>(a, nomask, vec, stream); break;
-    case 3201: blocks = launch_bwd_geometry<32, 1>(a, nomask, vec, stream); break;
-    case 6401: blocks = launch_bwd_geometry<64, 1>(a, nomask, vec, stream); break;
-    case 6402: blocks = launch_bwd_geometry<64, 2>(a, nomask, vec, stream); break;
-    case 6404: blocks = launch_bwd_geometry<64, 4>(a, nomask, vec, stream); break;
-    case 6408: blocks = launch_bwd_geometry<64, 8>(a, nomask, vec, stream); break;
-    default: blocks = launch_bwd_geometry<256, 4>(a, nomask, vec, stream); break;
+    case 1601: blocks = launch_bwd_geometry<16, 1>(a, nomask, vec, acc, stream); break;
+    case 3201: blocks = launch_bwd_geometry<32, 1>(a, nomask, vec, acc, stream); break;
+    case 6401: blocks = launch_bwd_geometry<64, 1>(a, nomask, vec, acc, stream); break;
+    case 6402: blocks = launch_bwd_geometry<64, 2>(a, nomask, vec, acc, stream); break;
+    case 6404: blocks = launch_bwd_geometry<64, 4>(a, nomask, vec, acc, stream); break;
+    case 6408: blocks = launch_bwd_geometry<64, 8>(a, nomask, vec, acc, stream); break;
+    default: blocks = launch_bwd_geometry<256, 4>(a, nomask, vec, acc, stream); break;
   }
   int st = launch_status("attnres backward");
   if (st != ATTNRES_OK) return st;
@@ -157,6 +157,22 @@ int check_scalars(float eps, float scale, bool need_eps) {
   if (need_eps && !(std::isfinite(eps) && eps > 0.0f)) return fail(ATTNRES_ERR_SCALAR, "eps must be finite and positive");
   if (!std::isfinite(scale)) return fail(ATTNRES_ERR_SCALAR, "scale must be finite");
   return ATTNRES_OK;
+}
+
+// Accumulate bits from one flag byte per source (nullptr: none); returns
+// whether any source accumulates.
+template <class Rows, class Grads>
+bool set_accumulate(BwdArgs<Rows, Grads>& a, const uint8_t* flags, int64_t n_sources) {
+  bool any = false;
+  for (auto& word : a.accumulate) word = 0;
+  if (!flags) return false;
+  for (int64_t s = 0; s < n_sources; ++s) {
+    if (flags[s]) {
+      a.accumulate[s >> 6] |= uint64_t{1} << (s & 63);
+      any = true;
+    }
+  }
+  return any;
 }
 
 // Workspace layout (FP32): [max_blocks, R] partial rows, [slices, R], [R] total.
@@ -213,18 +229,23 @@ int attnres_hip_packed_forward(const void* values, int64_t source_stride, int64_
   return launch_forward(a, vec, static_cast<hipStream_t>(stream));
 }
 
-int attnres_hip_packed_backward(const void* values, int64_t source_stride, int64_t row_stride,
-                                int64_t n_sources, int64_t n_tokens, int64_t width,
-                                const void* query, int64_t rank, float scale, const void* out,
-                                const int8_t* out_refine, const void* grad_out,
-                                const float* logit, const float* inv_rms, const float* stats,
-                                void* grad_values, void* grad_query, float* dq_workspace,
-                                int64_t dq_workspace_elems, void* stream) {
+}  // extern "C"
+
+namespace attnres_hip {
+namespace {
+
+int packed_backward(const void* values, int64_t source_stride, int64_t row_stride, int64_t n_sources,
+                    int64_t n_tokens, int64_t width, const void* query, int64_t rank, float scale,
+                    const void* out, const int8_t* out_refine, const void* grad_out, const float* logit,
+                    const float* inv_rms, const float* stats, void* grad_values, void* grad_query,
+                    float* dq_workspace, int64_t dq_workspace_elems, const uint8_t* accumulate, bool need_flags,
+                    void* stream) {
+  const char* name = need_flags ? "attnres_hip_packed_backward_accumulate" : "attnres_hip_packed_backward";
   int st = check_shape(n_sources, n_tokens, width, rank);
   if (st) return st;
   if (!values || !query || !out || !out_refine || !grad_out || !logit || !inv_rms || !stats ||
-      !grad_values || !grad_query || !dq_workspace)
-    return fail(ATTNRES_ERR_NULL_POINTER, "null pointer argument to attnres_hip_packed_backward");
+      !grad_values || !grad_query || !dq_workspace || (need_flags && !accumulate))
+    return fail(ATTNRES_ERR_NULL_POINTER, "null pointer argument to %s", name);
   if (source_stride < 0 || row_stride < 0) return fail(ATTNRES_ERR_STRIDE, "negative stride");
   if ((st = check_scalars(1.0f, scale, false))) return st;
   const int64_t need = workspace_elems(n_tokens, width, rank);
@@ -250,11 +271,42 @@ int attnres_hip_packed_backward(const void* values, int64_t source_stride, int64
   const bool vec = width % kVec == 0 && aligned16(values) && aligned16(out) && aligned16(out_refine) &&
                    aligned16(grad_out) && aligned16(grad_values) &&
                    (source_stride % kVec == 0 || n_sources == 1) && (row_stride % kVec == 0 || n_tokens == 1);
+  const bool acc = set_accumulate(a, accumulate, n_sources);
   const int64_t rows = grid_blocks(n_tokens, width, 0);
   float* slices = dq_workspace + rows * rank;
   float* dq32 = dq_workspace + (need - rank);
-  return launch_backward(a, vec, slices, dq32, static_cast<uint16_t*>(grad_query),
+  return launch_backward(a, vec, acc, slices, dq32, static_cast<uint16_t*>(grad_query),
                          static_cast<hipStream_t>(stream));
+}
+
+}  // namespace
+}  // namespace attnres_hip
+
+extern "C" {
+
+int attnres_hip_packed_backward(const void* values, int64_t source_stride, int64_t row_stride,
+                                int64_t n_sources, int64_t n_tokens, int64_t width,
+                                const void* query, int64_t rank, float scale, const void* out,
+                                const int8_t* out_refine, const void* grad_out,
+                                const float* logit, const float* inv_rms, const float* stats,
+                                void* grad_values, void* grad_query, float* dq_workspace,
+                                int64_t dq_workspace_elems, void* stream) {
+  return packed_backward(values, source_stride, row_stride, n_sources, n_tokens, width, query, rank, scale, out,
+                         out_refine, grad_out, logit, inv_rms, stats, grad_values, grad_query, dq_workspace,
+                         dq_workspace_elems, nullptr, false, stream);
+}
+
+int attnres_hip_packed_backward_accumulate(const void* values, int64_t source_stride, int64_t row_stride,
+                                           int64_t n_sources, int64_t n_tokens, int64_t width,
+                                           const void* query, int64_t rank, float scale, const void* out,
+                                           const int8_t* out_refine, const void* grad_out,
+                                           const float* logit, const float* inv_rms, const float* stats,
+                                           void* grad_values, void* grad_query, float* dq_workspace,
+                                           int64_t dq_workspace_elems, const uint8_t* accumulate,
+                                           void* stream) {
+  return packed_backward(values, source_stride, row_stride, n_sources, n_tokens, width, query, rank, scale, out,
+                         out_refine, grad_out, logit, inv_rms, stats, grad_values, grad_query, dq_workspace,
+                         dq_workspace_elems, accumulate, true, stream);
 }
 
 int attnres_hip_sources_forward(const void* const* sources, const int64_t* row_strides,
@@ -291,18 +343,23 @@ int attnres_hip_sources_forward(const void* const* sources, const int64_t* row_s
   return launch_forward(a, vec, static_cast<hipStream_t>(stream));
 }
 
-int attnres_hip_sources_backward(const void* const* sources, const int64_t* row_strides,
-                                 int64_t n_sources, int64_t n_tokens, int64_t width,
-                                 const void* query, int64_t rank, float scale, const void* out,
-                                 const int8_t* out_refine, const void* grad_out,
-                                 const float* logit, const float* inv_rms, const float* stats,
-                                 void* const* grad_sources, void* grad_query, float* dq_workspace,
-                                 int64_t dq_workspace_elems, void* stream) {
+}  // extern "C"
+
+namespace attnres_hip {
+namespace {
+
+int sources_backward(const void* const* sources, const int64_t* row_strides, int64_t n_sources,
+                     int64_t n_tokens, int64_t width, const void* query, int64_t rank, float scale,
+                     const void* out, const int8_t* out_refine, const void* grad_out, const float* logit,
+                     const float* inv_rms, const float* stats, void* const* grad_sources, void* grad_query,
+                     float* dq_workspace, int64_t dq_workspace_elems, const uint8_t* accumulate, bool need_flags,
+                     void* stream) {
+  const char* name = need_flags ? "attnres_hip_sources_backward_accumulate" : "attnres_hip_sources_backward";
   int st = check_shape(n_sources, n_tokens, width, rank);
   if (st) return st;
   if (!sources || !row_strides || !query || !out || !out_refine || !grad_out || !logit ||
-      !inv_rms || !stats || !grad_sources || !grad_query || !dq_workspace)
-    return fail(ATTNRES_ERR_NULL_POINTER, "null pointer argument to attnres_hip_sources_backward");
+      !inv_rms || !stats || !grad_sources || !grad_query || !dq_workspace || (need_flags && !accumulate))
+    return fail(ATTNRES_ERR_NULL_POINTER, "null pointer argument to %s", name);
   if ((st = check_scalars(1.0f, scale, false))) return st;
   const int64_t need = workspace_elems(n_tokens, width, rank);
   if (dq_workspace_elems < need)
@@ -333,11 +390,42 @@ int attnres_hip_sources_backward(const void* const* sources, const int64_t* row_
   a.width = static_cast<int>(width);
   a.rank = static_cast<int>(rank);
   a.scale = scale;
+  const bool acc = set_accumulate(a, accumulate, n_sources);
   const int64_t rows = grid_blocks(n_tokens, width, 0);
   float* slices = dq_workspace + rows * rank;
   float* dq32 = dq_workspace + (need - rank);
-  return launch_backward(a, vec, slices, dq32, static_cast<uint16_t*>(grad_query),
+  return launch_backward(a, vec, acc, slices, dq32, static_cast<uint16_t*>(grad_query),
                          static_cast<hipStream_t>(stream));
+}
+
+}  // namespace
+}  // namespace attnres_hip
+
+extern "C" {
+
+int attnres_hip_sources_backward(const void* const* sources, const int64_t* row_strides,
+                                 int64_t n_sources, int64_t n_tokens, int64_t width,
+                                 const void* query, int64_t rank, float scale, const void* out,
+                                 const int8_t* out_refine, const void* grad_out,
+                                 const float* logit, const float* inv_rms, const float* stats,
+                                 void* const* grad_sources, void* grad_query, float* dq_workspace,
+                                 int64_t dq_workspace_elems, void* stream) {
+  return sources_backward(sources, row_strides, n_sources, n_tokens, width, query, rank, scale, out, out_refine,
+                          grad_out, logit, inv_rms, stats, grad_sources, grad_query, dq_workspace,
+                          dq_workspace_elems, nullptr, false, stream);
+}
+
+int attnres_hip_sources_backward_accumulate(const void* const* sources, const int64_t* row_strides,
+                                            int64_t n_sources, int64_t n_tokens, int64_t width,
+                                            const void* query, int64_t rank, float scale, const void* out,
+                                            const int8_t* out_refine, const void* grad_out,
+                                            const float* logit, const float* inv_rms, const float* stats,
+                                            void* const* grad_sources, void* grad_query, float* dq_workspace,
+                                            int64_t dq_workspace_elems, const uint8_t* accumulate,
+                                            void* stream) {
+  return sources_backward(sources, row_strides, n_sources, n_tokens, width, query, rank, scale, out, out_refine,
+                          grad_out, logit, inv_rms, stats, grad_sources, grad_query, dq_workspace,
+                          dq_workspace_elems, accumulate, true, stream);
 }
 
 }  // extern "C"

@@ -95,6 +95,10 @@ struct BwdArgs {
   int width;
   int rank;
   float scale;
+  // Accumulating backward only: bit s set -> source s's gradient rows hold a
+  // gradient that dv is added to (bf16(old + dv)); clear -> dv is written.
+  uint64_t accumulate[(kMaxSources + 63) / 64];
+  __host__ __device__ bool accumulates(int s) const { return (accumulate[s >> 6] >> (s & 63)) & 1u; }
 };
 
 // ------------------------------------------------------------------ geometry
@@ -138,9 +142,10 @@ template <int G, int CH, class Rows>
 void launch_fwd_geometry(const FwdArgs<Rows>& a, bool nomask, bool vec, hipStream_t stream);
 
 // Enqueue the backward of geometry (G, CH); returns the grid size (the number
-// of dq partial rows written to a.partial).
+// of dq partial rows written to a.partial).  `acc`: the accumulating variant
+// (dv added to the gradient rows of the sources flagged in a.accumulate).
 template <int G, int CH, class Rows, class Grads>
-int64_t launch_bwd_geometry(const BwdArgs<Rows, Grads>& a, bool nomask, bool vec, hipStream_t stream);
+int64_t launch_bwd_geometry(const BwdArgs<Rows, Grads>& a, bool nomask, bool vec, bool acc, hipStream_t stream);
 
 #define ATTNRES_DECLARE_GEOMETRY(G, CH)                                                                  \
   extern template void launch_fwd_geometry<G, CH, PackedRows>(const FwdArgs<PackedRows>&, bool, bool,    \
@@ -148,9 +153,9 @@ int64_t launch_bwd_geometry(const BwdArgs<Rows, Grads>& a, bool nomask, bool vec
   extern template void launch_fwd_geometry<G, CH, ListRows>(const FwdArgs<ListRows>&, bool, bool,        \
                                                             hipStream_t);                                \
   extern template int64_t launch_bwd_geometry<G, CH, PackedRows, PackedGrads>(                           \
-      const BwdArgs<PackedRows, PackedGrads>&, bool, bool, hipStream_t);                                 \
+      const BwdArgs<PackedRows, PackedGrads>&, bool, bool, bool, hipStream_t);                           \
   extern template int64_t launch_bwd_geometry<G, CH, ListRows, ListGrads>(                               \
-      const BwdArgs<ListRows, ListGrads>&, bool, bool, hipStream_t);
+      const BwdArgs<ListRows, ListGrads>&, bool, bool, bool, hipStream_t);
 
 #define ATTNRES_FOR_EACH_GEOMETRY(X) X(16, 1) X(32, 1) X(64, 1) X(64, 2) X(64, 4) X(64, 8) X(256, 4)
 

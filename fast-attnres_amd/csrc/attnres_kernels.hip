@@ -586,7 +586,20 @@ __device__ __forceinline__ float token_delta(const TokenRows<CH>& t) {
 // right after a ring refill, and folded into delta on the token's last item
 // -- when the younger rows in the ring are still in flight -- so a token
 // switch does not drain the ring.
-template <int G, int CH, int NB, bool NOMASK, bool VEC, class Rows, class Grads>
+// The gradient rows of one token seen as rows of width D (for prefetching the
+// rows the accumulating backward adds to).
+template <class Grads>
+struct GradRows {
+  const Grads& grad;
+  int width;
+  __device__ __forceinline__ const uint16_t* row(int s, int64_t n) const { return grad.row(s, n, width); }
+};
+
+// ACC: the accumulating variant.  For a source whose bit is set in
+// a.accumulate, the item's gradient row is prefetched with its value row (a
+// second ring; other items load the idle row, so every load stays
+// unconditional) and dv is stored as bf16(old + dv).
+template <int G, int CH, int NB, bool NOMASK, bool VEC, bool ACC, class Rows, class Grads>
 __global__ void __launch_bounds__(kBlock) attnres_bwd_kernel(const BwdArgs<Rows, Grads> a) {
   static_assert(G <= 64 || G == kBlock, "a wide group is the whole workgroup");
   constexpr int kGroups = kBlock / G;
@@ -660,9 +673,15 @@ __global__ void __launch_bounds__(kBlock) attnres_bwd_kernel(const BwdArgs<Rows,
     u32x4 ring[NB][CH];
     float ring_z[NB];
     float ring_r[NB];
+    u32x4 ring_old[ACC ? NB : 1][CH];  // ACC: the gradient rows dv is added to
+    bool ring_acc[ACC ? NB : 1];
     auto refill_slot = [&](int j) __attribute__((always_inline)) {
       const bool live = ahead_item < last;
       refill<G, CH, VEC>(a.src, ahead, live, idle, lane, D, ring[j]);
+      if constexpr (ACC) {
+        ring_acc[j] = live && a.accumulates(ahead.source);
+        refill<G, CH, VEC>(GradRows<Grads>{a.grad, D}, ahead, ring_acc[j], idle, lane, D, ring_old[j]);
+      }
       const int64_t at_item = live ? ahead.token * S + ahead.source : 0;
       ring_z[j] = a.logit[at_item];
       ring_r[j] = a.inv_rms[at_item];
@@ -716,10 +735,15 @@ __global__ void __launch_bounds__(kBlock) attnres_bwd_kernel(const BwdArgs<Rows,
           const uint32_t kw = NOMASK ? w[k] : (w[k] & km[c][k]);
           const float k0 = bf16_lo(kw), k1 = bf16_hi(kw);
           const float g0 = __uint_as_float(gw[k] << lo_shift), g1 = __uint_as_float(gw[k] & hi_mask);
-          const float v0 = fmaf(cb, k0, fmaf(ca, qf[2 * k], p * g0));
-          const float v1 = fmaf(cb, k1, fmaf(ca, qf[2 * k + 1], p * g1));
+          float v0 = fmaf(cb, k0, fmaf(ca, qf[2 * k], p * g0));
+          float v1 = fmaf(cb, k1, fmaf(ca, qf[2 * k + 1], p * g1));
           dq[c][2 * k] = fmaf(ca, k0, dq[c][2 * k]);
           dq[c][2 * k + 1] = fmaf(ca, k1, dq[c][2 * k + 1]);
+          if constexpr (ACC) {
+            const uint32_t ow[4] = {ring_old[j][c].x, ring_old[j][c].y, ring_old[j][c].z, ring_old[j][c].w};
+            v0 = (ring_acc[j] ? bf16_lo(ow[k]) : 0.0f) + v0;
+            v1 = (ring_acc[j] ? bf16_hi(ow[k]) : 0.0f) + v1;
+          }
           out[k] = pack_bf16x2(v0, v1);
         }
         if (NOMASK || d0 < D) store_chunk<VEC>(grad_row, d0, D, u32x4{out[0], out[1], out[2], out[3]});
@@ -824,20 +848,26 @@ void launch_fwd_geometry(const FwdArgs<Rows>& a, bool nomask, bool vec, hipStrea
   }
 }
 
-template <int G, int CH, bool NOMASK, bool VEC, class Rows, class Grads>
+template <int G, int CH, bool NOMASK, bool VEC, bool ACC, class Rows, class Grads>
 int64_t launch_bwd(const BwdArgs<Rows, Grads>& a, hipStream_t stream) {
   const int64_t resident =
-      resident_blocks<&attnres_bwd_kernel<G, CH, bwd_ring<CH>(), NOMASK, VEC, Rows, Grads>>();
+      resident_blocks<&attnres_bwd_kernel<G, CH, bwd_ring<CH>(), NOMASK, VEC, ACC, Rows, Grads>>();
   const int64_t blocks = grid_blocks(a.n_tokens, a.width, resident);
-  hipLaunchKernelGGL((attnres_bwd_kernel<G, CH, bwd_ring<CH>(), NOMASK, VEC, Rows, Grads>),
+  hipLaunchKernelGGL((attnres_bwd_kernel<G, CH, bwd_ring<CH>(), NOMASK, VEC, ACC, Rows, Grads>),
                      dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream, a);
   return blocks;
 }
 
+template <int G, int CH, bool ACC, class Rows, class Grads>
+int64_t launch_bwd_variant(const BwdArgs<Rows, Grads>& a, bool nomask, bool vec, hipStream_t stream) {
+  if (nomask) return vec ? launch_bwd<G, CH, true, true, ACC>(a, stream) : launch_bwd<G, CH, true, false, ACC>(a, stream);
+  return vec ? launch_bwd<G, CH, false, true, ACC>(a, stream) : launch_bwd<G, CH, false, false, ACC>(a, stream);
+}
+
 template <int G, int CH, class Rows, class Grads>
-int64_t launch_bwd_geometry(const BwdArgs<Rows, Grads>& a, bool nomask, bool vec, hipStream_t stream) {
-  if (nomask) return vec ? launch_bwd<G, CH, true, true>(a, stream) : launch_bwd<G, CH, true, false>(a, stream);
-  return vec ? launch_bwd<G, CH, false, true>(a, stream) : launch_bwd<G, CH, false, false>(a, stream);
+int64_t launch_bwd_geometry(const BwdArgs<Rows, Grads>& a, bool nomask, bool vec, bool acc, hipStream_t stream) {
+  return acc ? launch_bwd_variant<G, CH, true>(a, nomask, vec, stream)
+             : launch_bwd_variant<G, CH, false>(a, nomask, vec, stream);
 }
 
 #if defined(ATTNRES_LANES) && defined(ATTNRES_CHUNKS)
@@ -846,9 +876,9 @@ template void launch_fwd_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, PackedRows>(con
 template void launch_fwd_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, ListRows>(const FwdArgs<ListRows>&, bool, bool,
                                                                            hipStream_t);
 template int64_t launch_bwd_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, PackedRows, PackedGrads>(
-    const BwdArgs<PackedRows, PackedGrads>&, bool, bool, hipStream_t);
+    const BwdArgs<PackedRows, PackedGrads>&, bool, bool, bool, hipStream_t);
 template int64_t launch_bwd_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, ListRows, ListGrads>(
-    const BwdArgs<ListRows, ListGrads>&, bool, bool, hipStream_t);
+    const BwdArgs<ListRows, ListGrads>&, bool, bool, bool, hipStream_t);
 #else
 #error "compile attnres_kernels.hip with -DATTNRES_LANES=<G> -DATTNRES_CHUNKS=<CH>"
 #endif

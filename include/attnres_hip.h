@@ -155,6 +155,44 @@ int attnres_hip_sources_backward(const void* const* sources,
                                  void* grad_query, float* dq_workspace,
                                  int64_t dq_workspace_elems, void* stream);
 
+/*
+ * Accumulating backward: the same arguments as the backward above, plus
+ * `accumulate`, a HOST array of n_sources flag bytes.  For a source whose
+ * flag is nonzero, its gradient rows must already hold a BF16 gradient, and
+ * the read's dv is added to it in the kernel (stored as bf16(old + dv), dv
+ * in FP32); other sources' gradient rows are overwritten as in the plain
+ * backward.  dq is written (not accumulated).  Several reads of the same
+ * sources can so sum their source gradients without separate add kernels
+ * (one extra read of the gradient rows instead of reading two buffers and
+ * writing a third).
+ *
+ * No counterpart launch in the reference: there, autograd sums the gradients
+ * of sources shared by several reads with separate add kernels after each
+ * read's backward.  Used by attnres.SharedSources.
+ */
+int attnres_hip_packed_backward_accumulate(const void* values, int64_t source_stride,
+                                           int64_t row_stride, int64_t n_sources,
+                                           int64_t n_tokens, int64_t width,
+                                           const void* query, int64_t rank, float scale,
+                                           const void* out, const int8_t* out_refine,
+                                           const void* grad_out, const float* logit,
+                                           const float* inv_rms, const float* stats,
+                                           void* grad_values, void* grad_query,
+                                           float* dq_workspace, int64_t dq_workspace_elems,
+                                           const uint8_t* accumulate, void* stream);
+
+int attnres_hip_sources_backward_accumulate(const void* const* sources,
+                                            const int64_t* row_strides, int64_t n_sources,
+                                            int64_t n_tokens, int64_t width,
+                                            const void* query, int64_t rank, float scale,
+                                            const void* out, const int8_t* out_refine,
+                                            const void* grad_out, const float* logit,
+                                            const float* inv_rms, const float* stats,
+                                            void* const* grad_sources,
+                                            void* grad_query, float* dq_workspace,
+                                            int64_t dq_workspace_elems,
+                                            const uint8_t* accumulate, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -20,7 +20,8 @@ from attnres import LearnedQuery, attnres
 
 
 def test_public_surface():
-    assert set(package.__all__) == {"attnres", "LearnedQuery", "__version__"}
+    # the reference's surface plus SharedSources (an addition with no reference counterpart)
+    assert set(package.__all__) == {"attnres", "LearnedQuery", "__version__", "SharedSources"}
     parameters = inspect.signature(attnres).parameters
     assert list(parameters) == ["values", "query", "eps", "scale"]
     assert parameters["eps"].kind is inspect.Parameter.KEYWORD_ONLY
@@ -201,3 +202,19 @@ def test_row_layout_flattening():
     assert ops.row_stride(single) == 5
     tensor, stride = ops.prepare_rows(base.transpose(0, 1))
     assert tensor.is_contiguous() and stride == 10
+
+
+def test_shared_sources_rejects_bad_inputs_on_the_host():
+    from attnres import SharedSources
+
+    cpu = [torch.zeros(4, 8, dtype=torch.bfloat16) for _ in range(2)]
+    with pytest.raises(RuntimeError, match="CUDA"):
+        SharedSources(cpu)
+    with pytest.raises(TypeError):
+        SharedSources([])
+    with pytest.raises(TypeError):
+        SharedSources(torch.zeros(2, 4, 8, dtype=torch.bfloat16))
+    with pytest.raises(TypeError, match="BF16"):
+        SharedSources([torch.zeros(4, 8), torch.zeros(4, 8)])
+    with pytest.raises(ValueError):
+        SharedSources([torch.zeros(4, 8, dtype=torch.bfloat16), torch.zeros(4, 9, dtype=torch.bfloat16)])

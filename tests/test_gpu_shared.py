@@ -1,0 +1,90 @@
+"""SharedSources on the GPU: several reads of one source list whose source
+gradients are summed inside the backward kernels.
+
+Compared with the same reads through ``attnres`` (autograd sums the
+per-read BF16 gradients with add kernels) and with the oracle: outputs and
+dq are bit-identical to ``attnres`` (same kernels); the source gradients
+agree to the rounding of a BF16 sum (the bank adds each read's FP32 dv to the
+running BF16 sum; autograd adds BF16-rounded dv) and match the oracle's
+summed gradients to the BF16 gate.  The shapes follow config c4 at a reduced
+token count (9 separately allocated sources, 3 reads) plus a masked width.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from attnres import SharedSources, attnres
+from helpers import compare
+from oracle.oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(sources=9, tokens=(2, 301), width=2048, rank=2048, reads=3, seed=31):
+    torch.manual_seed(seed)
+    src = [(torch.randn(*tokens, width, device="cuda") * (0.5 + s / 4)).to(torch.bfloat16).requires_grad_()
+           for s in range(sources)]
+    queries = [(torch.randn(rank, device="cuda") / math.sqrt(rank)).to(torch.bfloat16).requires_grad_()
+               for _ in range(reads)]
+    grads = [torch.randn(*tokens, width, device="cuda").to(torch.bfloat16) for _ in range(reads)]
+    scales = [1.0, 0.5, 2.0][:reads]
+    return src, queries, grads, scales
+
+
+def _run(read_fn, src, queries, grads, scales):
+    outs = [read_fn(q, s) for q, s in zip(queries, scales)]
+    loss = sum((o.float() * g.float()).sum() for o, g in zip(outs, grads))
+    params = (*src, *queries)
+    return outs, torch.autograd.grad(loss, params)
+
+
+@pytest.mark.parametrize("width,rank", [(2048, 2048), (1000, 96)], ids=["d2048_r2048", "d1000_r96"])
+def test_shared_sources_match_autograd_sums_and_the_oracle(width, rank):
+    src, queries, grads, scales = _case(width=width, rank=rank)
+    print(f"shared sources width={width} rank={rank}", flush=True)
+    bank = SharedSources(src)
+    outs_bank, grads_bank = _run(lambda q, s: bank.read(q, scale=s), src, queries, grads, scales)
+    outs_ref, grads_ref = _run(lambda q, s: attnres(tuple(src), q, scale=s), src, queries, grads, scales)
+    torch.cuda.synchronize()
+    count = len(src)
+    for a, b in zip(outs_bank, outs_ref):
+        assert torch.equal(a, b)
+    for a, b in zip(grads_bank[count:], grads_ref[count:]):  # dq: same kernels, same order
+        assert torch.equal(a, b)
+    for a, b in zip(grads_bank[:count], grads_ref[:count]):
+        # two BF16 roundings of partial sums apart at most, on the scale of the gradient
+        torch.testing.assert_close(a.float(), b.float(), rtol=2.0**-6, atol=2.0**-6 * float(b.float().abs().max()))
+    cpu_src = [t.detach().cpu().requires_grad_() for t in src]
+    cpu_q = [q.detach().cpu().requires_grad_() for q in queries]
+    outs_cpu = [oracle(tuple(cpu_src), q, scale=s) for q, s in zip(cpu_q, scales)]
+    loss = sum((o.float() * g.cpu().float()).sum() for o, g in zip(outs_cpu, grads))
+    grads_cpu = torch.autograd.grad(loss, (*cpu_src, *cpu_q))
+    for a, e in zip(grads_bank, grads_cpu):
+        compare(a, e)
+
+
+def test_each_backward_pass_starts_a_fresh_sum():
+    src, queries, grads, scales = _case(sources=4, tokens=(64,), width=512, rank=512, reads=2)
+    bank = SharedSources(src)
+    outs = [bank.read(q, scale=s) for q, s in zip(queries, scales)]
+    loss = sum((o.float() * g.float()).sum() for o, g in zip(outs, grads))
+    first = torch.autograd.grad(loss, src, retain_graph=True)
+    second = torch.autograd.grad(loss, src)
+    for a, b in zip(first, second):
+        assert torch.equal(a, b)
+
+
+def test_unused_reads_and_sources_without_grad():
+    src, queries, grads, scales = _case(sources=3, tokens=(40,), width=256, rank=64, reads=2)
+    src[1].requires_grad_(False)
+    bank = SharedSources(src)
+    used = bank.read(queries[0])
+    bank.read(queries[1])  # never reaches the loss: its backward does not run
+    g0, g2, gq = torch.autograd.grad((used.float() * grads[0].float()).sum(), (src[0], src[2], queries[0]))
+    ref = attnres(tuple(src), queries[0])
+    r0, r2, rq = torch.autograd.grad((ref.float() * grads[0].float()).sum(), (src[0], src[2], queries[0]))
+    assert torch.equal(g0, r0) and torch.equal(g2, r2) and torch.equal(gq, rq)

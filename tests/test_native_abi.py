@@ -19,7 +19,8 @@ _C_TYPES = {
     "void*": ctypes.c_void_p, "const void*": ctypes.c_void_p, "float*": ctypes.c_void_p,
     "const float*": ctypes.c_void_p, "int8_t*": ctypes.c_void_p, "const int8_t*": ctypes.c_void_p,
     "const void* const*": ctypes.c_void_p, "void* const*": ctypes.c_void_p,
-    "const int64_t*": ctypes.c_void_p, "int64_t": ctypes.c_int64, "float": ctypes.c_float,
+    "const int64_t*": ctypes.c_void_p, "const uint8_t*": ctypes.c_void_p, "int64_t": ctypes.c_int64,
+    "float": ctypes.c_float,
 }
 
 
@@ -120,3 +121,28 @@ def test_status_is_raised_with_the_library_message():
     _forward(width=9000)
     with pytest.raises(ValueError, match="width"):
         _native.check(_native.ERR_SHAPE, "attnres packed forward")
+
+
+def test_accumulating_backward_needs_its_flags_and_checks_like_the_plain_one():
+    """The accumulate entry points take the plain backward's arguments plus a
+    host array of flags; a missing array and the plain checks fail on the
+    host (no device work)."""
+    lib = _native.load()
+    need = lib.attnres_hip_dq_workspace_elems(4, 64, 16)
+    flags = (ctypes.c_uint8 * 3)(1, 0, 1)
+    common = (_FAKE, 16, 1.0, _FAKE, _FAKE, _FAKE, _FAKE, _FAKE, _FAKE)
+    status = lib.attnres_hip_packed_backward_accumulate(
+        _FAKE, 64, 64, 3, 4, 64, *common, _FAKE, _FAKE, _FAKE, need, None, None)
+    assert status == _native.ERR_NULL_POINTER
+    assert b"accumulate" in lib.attnres_hip_last_error()
+    status = lib.attnres_hip_packed_backward_accumulate(
+        _FAKE, 64, 64, 3, 4, 64, *common, _FAKE, _FAKE, _FAKE, need - 1, flags, None)
+    assert status == _native.ERR_WORKSPACE
+    pointers = (ctypes.c_void_p * 3)(_FAKE, _FAKE, _FAKE)
+    strides = (ctypes.c_int64 * 3)(64, 64, 64)
+    status = lib.attnres_hip_sources_backward_accumulate(
+        pointers, strides, 3, 4, 64, *common, pointers, _FAKE, _FAKE, need, None, None)
+    assert status == _native.ERR_NULL_POINTER
+    status = lib.attnres_hip_sources_backward_accumulate(
+        pointers, strides, 0, 4, 64, *common, pointers, _FAKE, _FAKE, need, flags, None)
+    assert status == _native.ERR_SHAPE
