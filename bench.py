@@ -339,43 +339,63 @@ def run_sweep(cfg: dict, steps: int, warmup: int) -> dict:
     }
 
 
-def run_model(cfg: dict, steps: int, warmup: int) -> dict:
-    """model: training steps of the Full-schedule causal LM (benchmarks/model.py)."""
+def run_model(cfg: dict, steps: int, warmup: int, variant: str = "both") -> dict:
+    """model: training steps of the Full-schedule causal LM (benchmarks/model.py).
+
+    ``variant`` "both" times the plain step (the line's value) and then the
+    source-bank step; "plain" or "bank" times one of them alone (for traces).
+    """
     import torch
 
     from benchmarks.model import TrainingConfig, make_model, training_step
 
     config = TrainingConfig(**{k: cfg[k] for k in ("layers", "width", "heads", "ffn", "batch", "sequence", "vocab")},
                             mode="full", source_layout="packed")
-    torch.manual_seed(0)
-    model = make_model(config, backend="kernel").cuda()
-    optimizer = torch.optim.AdamW(model.parameters(), lr=1e-4)
+    n_tokens = config.batch * config.sequence
     generator = torch.Generator(device="cuda").manual_seed(0)
     tokens = torch.randint(config.vocab, (config.batch, config.sequence), device="cuda", generator=generator)
     targets = torch.roll(tokens, -1, dims=1)
-    for _ in range(warmup):
-        training_step(model, optimizer, tokens, targets)
-    torch.cuda.synchronize()
-    start, stop = _event(), _event()
-    start.record()
-    for _ in range(steps):
-        loss = training_step(model, optimizer, tokens, targets)
-    stop.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(stop) / steps
-    n_tokens = config.batch * config.sequence
+
+    def time_steps(source_bank):
+        torch.manual_seed(0)
+        model = make_model(config, backend="kernel", source_bank=source_bank).cuda()
+        optimizer = torch.optim.AdamW(model.parameters(), lr=1e-4)
+        for _ in range(warmup):
+            training_step(model, optimizer, tokens, targets)
+        torch.cuda.synchronize()
+        start, stop = _event(), _event()
+        start.record()
+        for _ in range(steps):
+            loss = training_step(model, optimizer, tokens, targets)
+        stop.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) / steps, float(loss)
+
+    ms, loss = time_steps(False) if variant != "bank" else (None, None)
+    bank_ms, bank_loss = time_steps(True) if variant != "plain" else (None, None)
+
+    def rate(t):
+        return None if t is None else round(n_tokens / (t * 1e-3), 1)
+
+    def rounded(x, digits):
+        return None if x is None else round(x, digits)
+
     reads = 2 * config.layers
     read_bytes_per_step = sum(sum(read_bytes(s, n_tokens, config.width)) for s in range(2, reads + 2))
     return {
         "metric": "model: 24-layer Full-schedule causal LM training step (48 AttnRes reads, S=2..49), tokens/s",
-        "value": round(n_tokens / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps,
-        "warmup": warmup, "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak",
+        "value": rate(ms), "unit": "tokens/s", "n_gpus": 1, "steps": steps,
+        "warmup": warmup, "ms_per_step": rounded(ms, 3), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32 model, bf16 reads", "data": "synthetic tokens (seeded)",
         "config": {"workload": cfg["name"], "layers": config.layers, "width": config.width, "heads": config.heads,
                    "ffn": config.ffn, "batch": config.batch, "sequence": config.sequence, "vocab": config.vocab,
                    "reads_per_step": reads, "read_sources": f"2..{reads + 1}",
                    "attnres_algorithmic_bytes_per_step": read_bytes_per_step},
-        "loss": round(float(loss), 4),
+        "loss": rounded(loss, 4),
+        # the same step with the residual stream kept in an attnres.SourceBank (one BF16
+        # cast per source, prefix reads, FP32 gradient sums in the backward kernels)
+        "source_bank": {"ms_per_step": rounded(bank_ms, 3), "tokens_per_s": rate(bank_ms),
+                        "loss": rounded(bank_loss, 4)},
         "roofline": None,
         "cpu_baseline": None,
     }
@@ -390,6 +410,8 @@ def main(argv=None) -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU oracle time")
     parser.add_argument("--copy-probe", action="store_true")
+    parser.add_argument("--model-variant", choices=("both", "plain", "bank"), default="both",
+                        help="--config model: time the plain step, the source-bank step, or both")
     args = parser.parse_args(argv)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -413,8 +435,11 @@ def main(argv=None) -> int:
     cfg = CONFIGS[args.config]
     if args.config in ("c4", "c5", "model"):
         torch.cuda.set_device(0)
-        run = {"c4": run_block_schedule, "c5": run_sweep, "model": run_model}[args.config]
-        print(json.dumps(run(cfg, args.steps, args.warmup)), flush=True)
+        if args.config == "model":
+            result = run_model(cfg, args.steps, args.warmup, args.model_variant)
+        else:
+            result = {"c4": run_block_schedule, "c5": run_sweep}[args.config](cfg, args.steps, args.warmup)
+        print(json.dumps(result), flush=True)
         return 0
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)

@@ -17,6 +17,12 @@ The surrounding Transformer is ordinary PyTorch in the model's dtype; reads
 cast their sources to BF16 and their output back (reference `_read`,
 model.py:279-291).  ``backend`` is ``"kernel"`` (the HIP operator) or any
 callable with the ``attnres`` signature, e.g. the CPU oracle for parity tests.
+
+``source_bank=True`` (Full schedule, HIP backend; no reference counterpart)
+keeps the residual stream in an ``attnres.SourceBank``: each source is cast to
+BF16 once, reads are prefix views of one packed buffer, and the reads'
+backward sums every source's gradient in FP32 inside the kernels, instead of
+the per-read casts, stacks and autograd additions of the plain path.
 """
 
 from __future__ import annotations
@@ -114,10 +120,13 @@ class TransformerLayer(nn.Module):
 class CausalAttnResLM(nn.Module):
     """Small causal Transformer with Full or Block AttnRes residual reads."""
 
-    def __init__(self, config: TrainingConfig, backend: Backend = "kernel") -> None:
+    def __init__(self, config: TrainingConfig, backend: Backend = "kernel", *, source_bank: bool = False) -> None:
         super().__init__()
+        if source_bank and (backend != "kernel" or config.mode != "full"):
+            raise ValueError("source_bank needs the HIP backend and the Full schedule")
         self.config = config
         self.backend = backend
+        self.source_bank = bool(source_bank)
         self.token_embedding = nn.Embedding(config.vocab, config.width)
         self.position_embedding = nn.Parameter(torch.empty(config.sequence, config.width))
         self.layers = nn.ModuleList(TransformerLayer(config) for _ in range(config.layers))
@@ -157,7 +166,19 @@ class CausalAttnResLM(nn.Module):
         layer = self.layers[event // 2]
         return layer.attention(x) if event % 2 == 0 else layer.mlp(x)
 
+    def _forward_full_bank(self, embedded: Tensor) -> Tensor:
+        from attnres import SourceBank
+
+        bank = SourceBank(2 * self.config.layers + 1)
+        bank.push(embedded)
+        for event in range(2 * self.config.layers):
+            x = embedded if event == 0 else bank.read(self.queries[event - 1].to(torch.bfloat16)).to(embedded.dtype)
+            bank.push(self._sublayer(event, x))
+        return bank.read(self.queries[-1].to(torch.bfloat16)).to(embedded.dtype)
+
     def _forward_full(self, embedded: Tensor) -> Tensor:
+        if self.source_bank:
+            return self._forward_full_bank(embedded)
         sources = [embedded]
         for event in range(2 * self.config.layers):
             x = embedded if event == 0 else self.read(sources, self.queries[event - 1])
@@ -194,13 +215,13 @@ class CausalAttnResLM(nn.Module):
         return self.lm_head(hidden)
 
 
-def make_model(config: TrainingConfig, backend: Backend = "kernel") -> CausalAttnResLM:
+def make_model(config: TrainingConfig, backend: Backend = "kernel", *, source_bank: bool = False) -> CausalAttnResLM:
     """Construct a model with the given residual-read backend."""
     if not isinstance(config, TrainingConfig):
         raise TypeError("config must be a TrainingConfig")
     if not (backend == "kernel" or callable(backend)):
         raise ValueError("backend must be 'kernel' or a callable")
-    return CausalAttnResLM(config, backend)
+    return CausalAttnResLM(config, backend, source_bank=source_bank)
 
 
 def training_step(model: nn.Module, optimizer: torch.optim.Optimizer, tokens: Tensor, targets: Tensor,

@@ -12,6 +12,6 @@ __version__ = "2.0.1+mi355x.1"
 
 from .api import attnres
 from .modules import LearnedQuery
-from .shared import SharedSources
+from .shared import SharedSources, SourceBank
 
-__all__ = ["LearnedQuery", "SharedSources", "__version__", "attnres"]
+__all__ = ["LearnedQuery", "SharedSources", "SourceBank", "__version__", "attnres"]

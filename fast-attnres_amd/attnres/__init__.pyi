@@ -2,6 +2,7 @@ from torch import Tensor
 
 from .modules import LearnedQuery as LearnedQuery
 from .shared import SharedSources as SharedSources
+from .shared import SourceBank as SourceBank
 
 __version__: str
 
@@ -15,4 +16,4 @@ def attnres(
 ) -> Tensor: ...
 
 
-__all__ = ["LearnedQuery", "SharedSources", "__version__", "attnres"]
+__all__ = ["LearnedQuery", "SharedSources", "SourceBank", "__version__", "attnres"]

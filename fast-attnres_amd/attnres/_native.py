@@ -51,6 +51,10 @@ SIGNATURES = {
         _c_void_p, _i64, _i64, _i64, _i64, _i64, _c_void_p, _i64, _f32,
         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
         _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p]),
+    "attnres_hip_packed_backward_accumulate_f32": (ctypes.c_int, [
+        _c_void_p, _i64, _i64, _i64, _i64, _i64, _c_void_p, _i64, _f32,
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+        _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p]),
     "attnres_hip_sources_backward_accumulate": (ctypes.c_int, [
         _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _f32,
         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,

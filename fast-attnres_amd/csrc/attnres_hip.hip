@@ -17,12 +17,14 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <type_traits>
 
 #include "attnres_internal.h"
 
 namespace attnres_hip {
 
 ATTNRES_FOR_EACH_GEOMETRY(ATTNRES_DECLARE_GEOMETRY)
+ATTNRES_FOR_EACH_GEOMETRY(ATTNRES_DECLARE_GEOMETRY_F32)
 
 namespace {
 
@@ -126,6 +128,18 @@ int launch_forward(const FwdArgs<Rows>& a, bool vec, hipStream_t stream) {
   return launch_status("attnres forward");
 }
 
+// BF16 gradients: the plain or the accumulating kernel; FP32 gradient sums:
+// always the accumulating kernel (its first write leaves every bit clear).
+template <int G, int CH, class Rows, class Grads>
+int64_t launch_bwd_geometry_any(const BwdArgs<Rows, Grads>& a, bool nomask, bool vec, bool acc, hipStream_t stream) {
+  if constexpr (std::is_same_v<Grads, PackedGradsF32>) {
+    (void)acc;
+    return launch_bwd_geometry_f32<G, CH>(a, nomask, vec, stream);
+  } else {
+    return launch_bwd_geometry<G, CH>(a, nomask, vec, acc, stream);
+  }
+}
+
 template <class Rows, class Grads>
 int launch_backward(const BwdArgs<Rows, Grads>& a, bool vec, bool acc, float* slices, float* dq32, uint16_t* dq16,
                     hipStream_t stream) {
@@ -133,13 +147,13 @@ int launch_backward(const BwdArgs<Rows, Grads>& a, bool vec, bool acc, float* sl
   const bool nomask = no_mask(geo, a.width, a.rank);
   int64_t blocks = 0;
   switch (geo.lanes * 100 + geo.chunks) {
-    case 1601: blocks = launch_bwd_geometry<16, 1>(a, nomask, vec, acc, stream); break;
-    case 3201: blocks = launch_bwd_geometry<32, 1>(a, nomask, vec, acc, stream); break;
-    case 6401: blocks = launch_bwd_geometry<64, 1>(a, nomask, vec, acc, stream); break;
-    case 6402: blocks = launch_bwd_geometry<64, 2>(a, nomask, vec, acc, stream); break;
-    case 6404: blocks = launch_bwd_geometry<64, 4>(a, nomask, vec, acc, stream); break;
-    case 6408: blocks = launch_bwd_geometry<64, 8>(a, nomask, vec, acc, stream); break;
-    default: blocks = launch_bwd_geometry<256, 4>(a, nomask, vec, acc, stream); break;
+    case 1601: blocks = launch_bwd_geometry_any<16, 1>(a, nomask, vec, acc, stream); break;
+    case 3201: blocks = launch_bwd_geometry_any<32, 1>(a, nomask, vec, acc, stream); break;
+    case 6401: blocks = launch_bwd_geometry_any<64, 1>(a, nomask, vec, acc, stream); break;
+    case 6402: blocks = launch_bwd_geometry_any<64, 2>(a, nomask, vec, acc, stream); break;
+    case 6404: blocks = launch_bwd_geometry_any<64, 4>(a, nomask, vec, acc, stream); break;
+    case 6408: blocks = launch_bwd_geometry_any<64, 8>(a, nomask, vec, acc, stream); break;
+    default: blocks = launch_bwd_geometry_any<256, 4>(a, nomask, vec, acc, stream); break;
   }
   int st = launch_status("attnres backward");
   if (st != ATTNRES_OK) return st;
@@ -234,13 +248,16 @@ int attnres_hip_packed_forward(const void* values, int64_t source_stride, int64_
 namespace attnres_hip {
 namespace {
 
+template <class Grads = PackedGrads>
 int packed_backward(const void* values, int64_t source_stride, int64_t row_stride, int64_t n_sources,
                     int64_t n_tokens, int64_t width, const void* query, int64_t rank, float scale,
                     const void* out, const int8_t* out_refine, const void* grad_out, const float* logit,
                     const float* inv_rms, const float* stats, void* grad_values, void* grad_query,
                     float* dq_workspace, int64_t dq_workspace_elems, const uint8_t* accumulate, bool need_flags,
                     void* stream) {
-  const char* name = need_flags ? "attnres_hip_packed_backward_accumulate" : "attnres_hip_packed_backward";
+  constexpr bool kF32 = std::is_same_v<Grads, PackedGradsF32>;
+  const char* name = kF32 ? "attnres_hip_packed_backward_accumulate_f32"
+                     : need_flags ? "attnres_hip_packed_backward_accumulate" : "attnres_hip_packed_backward";
   int st = check_shape(n_sources, n_tokens, width, rank);
   if (st) return st;
   if (!values || !query || !out || !out_refine || !grad_out || !logit || !inv_rms || !stats ||
@@ -252,9 +269,13 @@ int packed_backward(const void* values, int64_t source_stride, int64_t row_strid
   if (dq_workspace_elems < need)
     return fail(ATTNRES_ERR_WORKSPACE, "dq workspace has %lld elements, needs %lld",
                 (long long)dq_workspace_elems, (long long)need);
-  BwdArgs<PackedRows, PackedGrads> a{};
+  BwdArgs<PackedRows, Grads> a{};
   a.src = PackedRows{static_cast<const uint16_t*>(values), source_stride, row_stride};
-  a.grad = PackedGrads{static_cast<uint16_t*>(grad_values), n_tokens * width};
+  if constexpr (kF32) {
+    a.grad = PackedGradsF32{static_cast<float*>(grad_values), n_tokens * width};
+  } else {
+    a.grad = PackedGrads{static_cast<uint16_t*>(grad_values), n_tokens * width};
+  }
   a.query = static_cast<const uint16_t*>(query);
   a.out = static_cast<const uint16_t*>(out);
   a.out_refine = out_refine;
@@ -307,6 +328,19 @@ int attnres_hip_packed_backward_accumulate(const void* values, int64_t source_st
   return packed_backward(values, source_stride, row_stride, n_sources, n_tokens, width, query, rank, scale, out,
                          out_refine, grad_out, logit, inv_rms, stats, grad_values, grad_query, dq_workspace,
                          dq_workspace_elems, accumulate, true, stream);
+}
+
+int attnres_hip_packed_backward_accumulate_f32(const void* values, int64_t source_stride, int64_t row_stride,
+                                               int64_t n_sources, int64_t n_tokens, int64_t width,
+                                               const void* query, int64_t rank, float scale, const void* out,
+                                               const int8_t* out_refine, const void* grad_out,
+                                               const float* logit, const float* inv_rms, const float* stats,
+                                               float* grad_sums, void* grad_query, float* dq_workspace,
+                                               int64_t dq_workspace_elems, const uint8_t* accumulate,
+                                               void* stream) {
+  return packed_backward<PackedGradsF32>(values, source_stride, row_stride, n_sources, n_tokens, width, query, rank,
+                                         scale, out, out_refine, grad_out, logit, inv_rms, stats, grad_sums,
+                                         grad_query, dq_workspace, dq_workspace_elems, accumulate, true, stream);
 }
 
 int attnres_hip_sources_forward(const void* const* sources, const int64_t* row_strides,

@@ -61,6 +61,16 @@ struct ListGrads {
   }
 };
 
+// FP32 gradient sums of packed sources: one contiguous [S, N, D] FP32 buffer
+// (the accumulating backward of a source bank writes or adds FP32 dv rows).
+struct PackedGradsF32 {
+  float* base;
+  int64_t source_stride;  // N * D
+  __device__ __forceinline__ float* row(int s, int64_t n, int d) const {
+    return base + s * source_stride + n * d;
+  }
+};
+
 template <class Rows>
 struct FwdArgs {
   Rows src;
@@ -156,6 +166,15 @@ int64_t launch_bwd_geometry(const BwdArgs<Rows, Grads>& a, bool nomask, bool vec
       const BwdArgs<PackedRows, PackedGrads>&, bool, bool, bool, hipStream_t);                           \
   extern template int64_t launch_bwd_geometry<G, CH, ListRows, ListGrads>(                               \
       const BwdArgs<ListRows, ListGrads>&, bool, bool, bool, hipStream_t);
+
+// The accumulating backward into FP32 gradient sums (packed sources only).
+template <int G, int CH>
+int64_t launch_bwd_geometry_f32(const BwdArgs<PackedRows, PackedGradsF32>& a, bool nomask, bool vec,
+                                hipStream_t stream);
+
+#define ATTNRES_DECLARE_GEOMETRY_F32(G, CH)                                                          \
+  extern template int64_t launch_bwd_geometry_f32<G, CH>(const BwdArgs<PackedRows, PackedGradsF32>&, \
+                                                         bool, bool, hipStream_t);
 
 #define ATTNRES_FOR_EACH_GEOMETRY(X) X(16, 1) X(32, 1) X(64, 1) X(64, 2) X(64, 4) X(64, 8) X(256, 4)
 

@@ -46,6 +46,7 @@
 
 #include <cmath>
 #include <cstdint>
+#include <type_traits>
 
 #include "attnres_internal.h"
 
@@ -54,6 +55,7 @@ namespace attnres_hip {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 // ------------------------------------------------------------- BF16 helpers
@@ -586,6 +588,28 @@ __device__ __forceinline__ float token_delta(const TokenRows<CH>& t) {
 // right after a ring refill, and folded into delta on the token's last item
 // -- when the younger rows in the ring are still in flight -- so a token
 // switch does not drain the ring.
+// One FP32 row (this lane's chunks, two 16-byte words each), unconditional
+// like load_row: chunks at or beyond D read the row start (VEC) or clamped
+// elements.  VEC requires 16-byte aligned rows and D % 8 == 0.
+template <int G, int CH, bool VEC>
+__device__ __forceinline__ void load_row_f32(const float* __restrict__ row, int lane, int D, u32x4 (&raw)[2 * CH]) {
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int d0 = chunk_start<G>(c, lane);
+    if constexpr (VEC) {
+      const int at = d0 < D ? d0 : 0;
+      raw[2 * c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(row + at));
+      raw[2 * c + 1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(row + at + 4));
+    } else {
+      uint32_t w[kVec];
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) w[e] = __float_as_uint(row[min(d0 + e, D - 1)]);
+      raw[2 * c] = u32x4{w[0], w[1], w[2], w[3]};
+      raw[2 * c + 1] = u32x4{w[4], w[5], w[6], w[7]};
+    }
+  }
+}
+
 // The gradient rows of one token seen as rows of width D (for prefetching the
 // rows the accumulating backward adds to).
 template <class Grads>
@@ -599,8 +623,12 @@ struct GradRows {
 // a.accumulate, the item's gradient row is prefetched with its value row (a
 // second ring; other items load the idle row, so every load stays
 // unconditional) and dv is stored as bf16(old + dv).
+// With PackedGradsF32 gradients (a source bank's FP32 sums) the rows are FP32:
+// dv is written, or added, without BF16 rounding.
 template <int G, int CH, int NB, bool NOMASK, bool VEC, bool ACC, class Rows, class Grads>
 __global__ void __launch_bounds__(kBlock) attnres_bwd_kernel(const BwdArgs<Rows, Grads> a) {
+  constexpr bool kF32 = std::is_same_v<Grads, PackedGradsF32>;
+  static_assert(!kF32 || ACC, "FP32 gradient sums use the accumulating variant");
   static_assert(G <= 64 || G == kBlock, "a wide group is the whole workgroup");
   constexpr int kGroups = kBlock / G;
   __shared__ float xred[xred_floats<G>(1)];
@@ -673,14 +701,20 @@ __global__ void __launch_bounds__(kBlock) attnres_bwd_kernel(const BwdArgs<Rows,
     u32x4 ring[NB][CH];
     float ring_z[NB];
     float ring_r[NB];
-    u32x4 ring_old[ACC ? NB : 1][CH];  // ACC: the gradient rows dv is added to
+    u32x4 ring_old[ACC ? NB : 1][kF32 ? 2 * CH : CH];  // ACC: the gradient rows dv is added to
     bool ring_acc[ACC ? NB : 1];
     auto refill_slot = [&](int j) __attribute__((always_inline)) {
       const bool live = ahead_item < last;
       refill<G, CH, VEC>(a.src, ahead, live, idle, lane, D, ring[j]);
       if constexpr (ACC) {
         ring_acc[j] = live && a.accumulates(ahead.source);
-        refill<G, CH, VEC>(GradRows<Grads>{a.grad, D}, ahead, ring_acc[j], idle, lane, D, ring_old[j]);
+        if constexpr (kF32) {
+          // idle: row (0, 0) of the FP32 buffer (always 4*D bytes, cache-resident)
+          const float* row = ring_acc[j] ? a.grad.row(ahead.source, ahead.token, D) : a.grad.row(0, 0, D);
+          load_row_f32<G, CH, VEC>(row, lane, D, ring_old[j]);
+        } else {
+          refill<G, CH, VEC>(GradRows<Grads>{a.grad, D}, ahead, ring_acc[j], idle, lane, D, ring_old[j]);
+        }
       }
       const int64_t at_item = live ? ahead.token * S + ahead.source : 0;
       ring_z[j] = a.logit[at_item];
@@ -715,7 +749,7 @@ __global__ void __launch_bounds__(kBlock) attnres_bwd_kernel(const BwdArgs<Rows,
       const float dz = p * (dw[0] - delta);
       const float ca = inv_rms * (dz * scale);                  // on q; dq += ca * key
       const float cb = -(inv_rms * inv_rms) * (dz * z * inv_R);  // on the key coordinates
-      uint16_t* grad_row = a.grad.row(s, token, D);
+      auto* grad_row = a.grad.row(s, token, D);
       // dO is unpacked per item with a shift and mask the compiler cannot
       // prove loop-invariant (s >= 0, so both equal the constants): a hoisted
       // unpacked copy of dO would cost 32 registers per lane.
@@ -730,6 +764,7 @@ __global__ void __launch_bounds__(kBlock) attnres_bwd_kernel(const BwdArgs<Rows,
         const float4 qb = *reinterpret_cast<const float4*>(&q_lds[d0 + 4]);
         const float qf[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
         uint32_t out[4];
+        float outf[kF32 ? kVec : 1];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           const uint32_t kw = NOMASK ? w[k] : (w[k] & km[c][k]);
@@ -739,14 +774,37 @@ __global__ void __launch_bounds__(kBlock) attnres_bwd_kernel(const BwdArgs<Rows,
           float v1 = fmaf(cb, k1, fmaf(ca, qf[2 * k + 1], p * g1));
           dq[c][2 * k] = fmaf(ca, k0, dq[c][2 * k]);
           dq[c][2 * k + 1] = fmaf(ca, k1, dq[c][2 * k + 1]);
-          if constexpr (ACC) {
-            const uint32_t ow[4] = {ring_old[j][c].x, ring_old[j][c].y, ring_old[j][c].z, ring_old[j][c].w};
-            v0 = (ring_acc[j] ? bf16_lo(ow[k]) : 0.0f) + v0;
-            v1 = (ring_acc[j] ? bf16_hi(ow[k]) : 0.0f) + v1;
+          if constexpr (kF32) {
+            const u32x4& ow = ring_old[j][2 * c + (k >> 1)];
+            const uint32_t o0 = (k & 1) ? ow.z : ow.x, o1 = (k & 1) ? ow.w : ow.y;
+            outf[2 * k] = (ring_acc[j] ? __uint_as_float(o0) : 0.0f) + v0;
+            outf[2 * k + 1] = (ring_acc[j] ? __uint_as_float(o1) : 0.0f) + v1;
+          } else {
+            if constexpr (ACC) {
+              const uint32_t ow[4] = {ring_old[j][c].x, ring_old[j][c].y, ring_old[j][c].z, ring_old[j][c].w};
+              v0 = (ring_acc[j] ? bf16_lo(ow[k]) : 0.0f) + v0;
+              v1 = (ring_acc[j] ? bf16_hi(ow[k]) : 0.0f) + v1;
+            }
+            out[k] = pack_bf16x2(v0, v1);
           }
-          out[k] = pack_bf16x2(v0, v1);
         }
-        if (NOMASK || d0 < D) store_chunk<VEC>(grad_row, d0, D, u32x4{out[0], out[1], out[2], out[3]});
+        if constexpr (kF32) {
+          if constexpr (VEC) {
+            if (NOMASK || d0 < D) {
+              __builtin_nontemporal_store(f32x4{outf[0], outf[1], outf[2], outf[3]},
+                                          reinterpret_cast<f32x4*>(grad_row + d0));
+              __builtin_nontemporal_store(f32x4{outf[4], outf[5], outf[6], outf[7]},
+                                          reinterpret_cast<f32x4*>(grad_row + d0 + 4));
+            }
+          } else {
+#pragma unroll
+            for (int e = 0; e < kVec; ++e) {
+              if (d0 + e < D) grad_row[d0 + e] = outf[e];
+            }
+          }
+        } else if (NOMASK || d0 < D) {
+          store_chunk<VEC>(grad_row, d0, D, u32x4{out[0], out[1], out[2], out[3]});
+        }
       }
 
       if (refill) {
@@ -870,6 +928,12 @@ int64_t launch_bwd_geometry(const BwdArgs<Rows, Grads>& a, bool nomask, bool vec
              : launch_bwd_variant<G, CH, false>(a, nomask, vec, stream);
 }
 
+template <int G, int CH>
+int64_t launch_bwd_geometry_f32(const BwdArgs<PackedRows, PackedGradsF32>& a, bool nomask, bool vec,
+                                hipStream_t stream) {
+  return launch_bwd_variant<G, CH, true>(a, nomask, vec, stream);
+}
+
 #if defined(ATTNRES_LANES) && defined(ATTNRES_CHUNKS)
 template void launch_fwd_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, PackedRows>(const FwdArgs<PackedRows>&, bool,
                                                                              bool, hipStream_t);
@@ -879,6 +943,8 @@ template int64_t launch_bwd_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, PackedRows, 
     const BwdArgs<PackedRows, PackedGrads>&, bool, bool, bool, hipStream_t);
 template int64_t launch_bwd_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, ListRows, ListGrads>(
     const BwdArgs<ListRows, ListGrads>&, bool, bool, bool, hipStream_t);
+template int64_t launch_bwd_geometry_f32<ATTNRES_LANES, ATTNRES_CHUNKS>(const BwdArgs<PackedRows, PackedGradsF32>&,
+                                                                        bool, bool, hipStream_t);
 #else
 #error "compile attnres_kernels.hip with -DATTNRES_LANES=<G> -DATTNRES_CHUNKS=<CH>"
 #endif

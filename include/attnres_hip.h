@@ -181,6 +181,24 @@ int attnres_hip_packed_backward_accumulate(const void* values, int64_t source_st
                                            float* dq_workspace, int64_t dq_workspace_elems,
                                            const uint8_t* accumulate, void* stream);
 
+/*
+ * Accumulating packed backward into FP32 gradient sums: as
+ * attnres_hip_packed_backward_accumulate, but `grad_sums` is a contiguous FP32
+ * [S, N, D] buffer and dv is written (flag 0) or added (flag nonzero) in FP32,
+ * with no BF16 rounding.  For a source bank whose sources receive the sum of
+ * many reads' gradients (attnres.SourceBank).  No counterpart in the reference.
+ */
+int attnres_hip_packed_backward_accumulate_f32(const void* values, int64_t source_stride,
+                                               int64_t row_stride, int64_t n_sources,
+                                               int64_t n_tokens, int64_t width,
+                                               const void* query, int64_t rank, float scale,
+                                               const void* out, const int8_t* out_refine,
+                                               const void* grad_out, const float* logit,
+                                               const float* inv_rms, const float* stats,
+                                               float* grad_sums, void* grad_query,
+                                               float* dq_workspace, int64_t dq_workspace_elems,
+                                               const uint8_t* accumulate, void* stream);
+
 int attnres_hip_sources_backward_accumulate(const void* const* sources,
                                             const int64_t* row_strides, int64_t n_sources,
                                             int64_t n_tokens, int64_t width,

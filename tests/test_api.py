@@ -21,7 +21,7 @@ from attnres import LearnedQuery, attnres
 
 def test_public_surface():
     # the reference's surface plus SharedSources (an addition with no reference counterpart)
-    assert set(package.__all__) == {"attnres", "LearnedQuery", "__version__", "SharedSources"}
+    assert set(package.__all__) == {"attnres", "LearnedQuery", "__version__", "SharedSources", "SourceBank"}
     parameters = inspect.signature(attnres).parameters
     assert list(parameters) == ["values", "query", "eps", "scale"]
     assert parameters["eps"].kind is inspect.Parameter.KEYWORD_ONLY

@@ -83,3 +83,19 @@ def test_training_steps_reduce_the_loss():
     losses = [float(training_step(model, optimizer, tokens, targets)) for _ in range(12)]
     assert all(torch.isfinite(torch.tensor(losses)))
     assert losses[-1] < losses[0]
+
+
+def test_source_bank_model_matches_the_plain_model():
+    config = _config("full", "packed", "standard")
+    torch.manual_seed(37)
+    plain = make_model(config, backend="kernel").cuda()
+    banked = make_model(config, backend="kernel", source_bank=True).cuda()
+    banked.load_state_dict(plain.state_dict())
+    tokens = torch.randint(config.vocab, (config.batch, config.sequence), device="cuda")
+    a, b = plain(tokens), banked(tokens)
+    assert torch.equal(a, b)
+    weight = torch.randn_like(a)
+    (a * weight).sum().backward()
+    (b * weight).sum().backward()
+    for (name, p), q in zip(plain.named_parameters(), banked.parameters()):
+        assert _relative_error(q.grad, p.grad) < 2e-2, name
