@@ -73,6 +73,8 @@ CONFIGS = {
                name="block-schedule list S=9 N=32768 D=2048 R=2048, 3 reads sharing the sources"),
     "c5": dict(sources=48, batch=(16384,), widths=(1024, 4096),
                name="24-layer full-schedule sweep S=1..48 N=16384 D in {1024,4096} R in {D,D/4} packed"),
+    "policy": dict(sources=3, batch=(16384,), widths=(1024, 2048, 4096), rounds=5,
+                   name="save/recompute policy: reads of S=1..3 at N=16384, D in {1024,2048,4096}, R=D, packed"),
     "model": dict(layers=24, width=1024, heads=16, ffn=2816, batch=16, sequence=1024, vocab=8192,
                   name="24-layer Full-schedule causal LM training step, D=1024, 16x1024 tokens, FP32 outside the reads"),
 }
@@ -339,6 +341,78 @@ def run_sweep(cfg: dict, steps: int, warmup: int) -> dict:
     }
 
 
+def run_policy(cfg: dict, steps: int, warmup: int) -> dict:
+    """policy: fwd+bwd of small reads (S <= 3) with the output refinement saved
+    (the streaming backward reads out + refinement) and without it (the
+    recompute backward derives delta from the value rows); interleaved rounds,
+    best round per variant.  The ops are called directly so the two variants
+    differ only in the kernels."""
+    import torch
+
+    from attnres import _ops
+
+    device = torch.device("cuda:0")
+    tokens = cfg["batch"][0]
+    rows, ratios = [], []
+    for width in cfg["widths"]:
+        values, query, grad_out = make_inputs(dict(sources=cfg["sources"], batch=(tokens,), width=width, rank=width),
+                                              device, seed=width)
+        for sources in range(1, cfg["sources"] + 1):
+            packed = values[:sources]
+
+            def read(save, marks=None):
+                out, refine, logit, inv_rms, stats = _ops.packed_forward_impl(packed, query, 2**-23, 1.0, save)
+                if marks is not None:
+                    marks.record()
+                return _ops.packed_backward(packed, query, out, refine, grad_out, logit, inv_rms, stats, 1.0)
+
+            best = {True: float("inf"), False: float("inf")}
+            split = {True: (0.0, 0.0), False: (0.0, 0.0)}  # (fwd, bwd) ms of the best round
+            for save in (True, False):
+                for _ in range(warmup):
+                    read(save)
+            for _ in range(cfg["rounds"]):
+                for save in (True, False):
+                    events = [(_event(), _event(), _event()) for _ in range(steps)]
+                    for begin, middle, end in events:
+                        begin.record()
+                        read(save, middle)
+                        end.record()
+                    torch.cuda.synchronize()
+                    fwd = sum(b.elapsed_time(m) for b, m, _ in events) / steps
+                    bwd = sum(m.elapsed_time(e) for _, m, e in events) / steps
+                    if fwd + bwd < best[save]:
+                        best[save], split[save] = fwd + bwd, (fwd, bwd)
+            fwd_bytes, bwd_bytes = read_bytes(sources, tokens, width)
+            algorithmic = fwd_bytes + bwd_bytes
+            ratio = best[True] / best[False]
+            ratios.append(ratio)
+            rows.append({"width": width, "sources": sources,
+                         "save_us": round(best[True] * 1e3, 2), "recompute_us": round(best[False] * 1e3, 2),
+                         "speedup": round(ratio, 3),
+                         "save_fwd_bwd_us": [round(t * 1e3, 2) for t in split[True]],
+                         "recompute_fwd_bwd_us": [round(t * 1e3, 2) for t in split[False]],
+                         "recompute_TB/s": round(algorithmic / (best[False] * 1e-3) / 1e12, 3),
+                         "recompute_bwd_TB/s": round(bwd_bytes / (split[False][1] * 1e-3) / 1e12, 3),
+                         "save_TB/s": round(algorithmic / (best[True] * 1e-3) / 1e12, 3),
+                         "saved_state_bytes": {"save": 3 * tokens * width, "recompute": 0}})
+        del values, grad_out
+        torch.cuda.empty_cache()
+    value = math.exp(sum(math.log(r) for r in ratios) / len(ratios))
+    return {
+        "metric": "save/recompute policy: fwd+bwd time of reads with S<=3, saved-refinement path over recompute path "
+                  "(geometric mean speedup)",
+        "value": round(value, 4), "unit": "x", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "storage_dtype": "bf16", "data": "synthetic (seeded; per-source std U[0.5,4], 1% channels x8)",
+        "config": {"workload": cfg["name"], "tokens": tokens, "layout": "packed", "rounds": cfg["rounds"],
+                   "bytes": "algorithmic TB/s counts (2S+2) N D forward + (4S+2) N D backward for both paths"},
+        "reads": rows,
+        "roofline": None,
+        "cpu_baseline": None,
+    }
+
+
 def run_model(cfg: dict, steps: int, warmup: int, variant: str = "both") -> dict:
     """model: training steps of the Full-schedule causal LM (benchmarks/model.py).
 
@@ -433,12 +507,13 @@ def main(argv=None) -> int:
 
     _native.load()  # fail loudly if the HIP library is missing
     cfg = CONFIGS[args.config]
-    if args.config in ("c4", "c5", "model"):
+    if args.config in ("c4", "c5", "model", "policy"):
         torch.cuda.set_device(0)
         if args.config == "model":
             result = run_model(cfg, args.steps, args.warmup, args.model_variant)
         else:
-            result = {"c4": run_block_schedule, "c5": run_sweep}[args.config](cfg, args.steps, args.warmup)
+            run = {"c4": run_block_schedule, "c5": run_sweep, "policy": run_policy}[args.config]
+            result = run(cfg, args.steps, args.warmup)
         print(json.dumps(result), flush=True)
         return 0
     device = torch.device("cuda:0")

@@ -21,11 +21,16 @@ caller's device; the kernels run on the current stream and the C ABI never
 allocates or synchronises, so the ops are safe under ``torch.compile``
 (opaque custom ops with fake kernels) and HIP/CUDA graph capture.
 
-Saved for backward: the inputs, the BF16 output plus one refinement byte
-per element (together the FP32 mix to ulp/512, for ``delta = <dO, o>``) and
-the small statistics.  The reference instead keeps an FP32 copy of the
-output (`fixed_tail.py:917-919`): four extra bytes per element written in
-the forward and read in the backward instead of one.
+Saved for backward: the inputs, the small statistics and -- for reads of
+more than ``RECOMPUTE_MAX_SOURCES`` sources -- the BF16 output plus one
+refinement byte per element (together the FP32 mix to ulp/512, for
+``delta = <dO, o>``).  Smaller reads save neither: ``out_refine`` is
+``[0, D]`` and their backward derives delta from the value rows it reads
+anyway.  The reference makes the same structural choice
+(`fla_full_sources._should_save_mixed`, `fla_full_sources.py:146-161`:
+recompute for S <= 3) but saves an FP32 copy of the output for larger reads
+(`fixed_tail.py:917-919`): four extra bytes per element written in the
+forward and read in the backward instead of one.
 """
 
 from __future__ import annotations
@@ -41,6 +46,24 @@ from . import _native
 
 _F32 = torch.float32
 _BF16 = torch.bfloat16
+
+# Save/recompute policy (attnres_hip.h ATTNRES_RECOMPUTE_MAX_SOURCES).
+RECOMPUTE_MAX_SOURCES = 3
+
+
+def saves_refinement(sources: int) -> bool:
+    """Whether a read of ``sources`` sources saves its output refinement for
+    the backward (else the backward recomputes delta from the value rows;
+    reference `fla_full_sources._should_save_mixed`, `fla_full_sources.py:146-161`)."""
+    return sources > RECOMPUTE_MAX_SOURCES
+
+
+def _refine_rows(sources: int, tokens: int) -> int:
+    return tokens if saves_refinement(sources) else 0
+
+
+def _pointer(tensor: Tensor) -> int | None:
+    return tensor.data_ptr() if tensor.numel() else None
 _OP_TAGS = (torch.Tag.flexible_layout,) if hasattr(torch.Tag, "flexible_layout") else ()
 
 
@@ -105,34 +128,41 @@ def _dq_workspace(lib, n_tokens: int, width: int, rank: int, device) -> Tensor:
 
 # ------------------------------------------------------------------ packed
 
-@torch.library.custom_op("attnres_hip::packed_forward", mutates_args=(),
-                         device_types="cuda", tags=_OP_TAGS)
-def packed_forward(values: Tensor, query: Tensor, eps: float,
-                   scale: float) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+def packed_forward_impl(values: Tensor, query: Tensor, eps: float, scale: float,
+                        save: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """The packed forward launch; ``save`` chooses whether the refinement is
+    stored (``out_refine`` ``[N, D]``) or not (``[0, D]``)."""
     lib = _native.load()
     values = _unit_feature_stride(values)
     query = _contiguous(query)
     sources, tokens, width = (int(size) for size in values.shape)
     device = values.device
     out = torch.empty((tokens, width), device=device, dtype=_BF16)
-    out_refine = torch.empty((tokens, width), device=device, dtype=torch.int8)
+    out_refine = torch.empty((tokens if save else 0, width), device=device, dtype=torch.int8)
     logit = torch.empty((tokens, sources), device=device, dtype=_F32)
     inv_rms = torch.empty((tokens, sources), device=device, dtype=_F32)
     stats = torch.empty((2, tokens), device=device, dtype=_F32)
     with torch.cuda.device(device):
         status = lib.attnres_hip_packed_forward(
             values.data_ptr(), values.stride(0), values.stride(1), sources, tokens, width,
-            query.data_ptr(), query.numel(), eps, scale, out.data_ptr(), out_refine.data_ptr(),
+            query.data_ptr(), query.numel(), eps, scale, out.data_ptr(), _pointer(out_refine),
             logit.data_ptr(), inv_rms.data_ptr(), stats.data_ptr(), _stream(device))
     _native.check(status, "attnres packed forward")
     return out, out_refine, logit, inv_rms, stats
+
+
+@torch.library.custom_op("attnres_hip::packed_forward", mutates_args=(),
+                         device_types="cuda", tags=_OP_TAGS)
+def packed_forward(values: Tensor, query: Tensor, eps: float,
+                   scale: float) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    return packed_forward_impl(values, query, eps, scale, saves_refinement(int(values.shape[0])))
 
 
 @packed_forward.register_fake
 def _packed_forward_fake(values, query, eps, scale):
     sources, tokens, width = values.shape
     return (values.new_empty((tokens, width)),
-            values.new_empty((tokens, width), dtype=torch.int8),
+            values.new_empty((_refine_rows(sources, tokens), width), dtype=torch.int8),
             values.new_empty((tokens, sources), dtype=_F32),
             values.new_empty((tokens, sources), dtype=_F32),
             values.new_empty((2, tokens), dtype=_F32))
@@ -148,6 +178,7 @@ def packed_backward(values: Tensor, query: Tensor, out: Tensor, out_refine: Tens
     query = _contiguous(query)
     out = _contiguous(out)
     grad_out = _contiguous(grad_out.to(_BF16))
+    recompute = out_refine.numel() == 0  # nothing saved: delta from the value rows
     sources, tokens, width = (int(size) for size in values.shape)
     rank = query.numel()
     device = values.device
@@ -157,7 +188,8 @@ def packed_backward(values: Tensor, query: Tensor, out: Tensor, out_refine: Tens
     with torch.cuda.device(device):
         status = lib.attnres_hip_packed_backward(
             values.data_ptr(), values.stride(0), values.stride(1), sources, tokens, width,
-            query.data_ptr(), rank, scale, out.data_ptr(), _contiguous(out_refine).data_ptr(),
+            query.data_ptr(), rank, scale, None if recompute else out.data_ptr(),
+            None if recompute else _contiguous(out_refine).data_ptr(),
             grad_out.data_ptr(), _contiguous(logit).data_ptr(), _contiguous(inv_rms).data_ptr(),
             _contiguous(stats).data_ptr(), grad_values.data_ptr(), grad_query.data_ptr(),
             workspace.data_ptr(), workspace.numel(), _stream(device))
@@ -177,7 +209,9 @@ def _packed_setup_context(ctx: Any, inputs: tuple, output: tuple) -> None:
     out, out_refine, logit, inv_rms, stats = output
     ctx.mark_non_differentiable(out_refine, logit, inv_rms, stats)
     ctx.set_materialize_grads(False)
-    ctx.save_for_backward(values, query, out, out_refine, logit, inv_rms, stats)
+    # recompute policy: the output is not needed (the empty refinement stands in)
+    saved_out = out if out_refine.numel() else out_refine
+    ctx.save_for_backward(values, query, saved_out, out_refine, logit, inv_rms, stats)
     ctx.scale = float(scale)
 
 
@@ -221,10 +255,9 @@ def _source_table(sources: list[Tensor]) -> tuple[list[Tensor], Any, Any]:
     return prepared, pointers, row_strides
 
 
-@torch.library.custom_op("attnres_hip::sources_forward", mutates_args=(),
-                         device_types="cuda", tags=_OP_TAGS)
-def sources_forward(sources: list[Tensor], query: Tensor, eps: float,
-                    scale: float) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+def sources_forward_impl(sources: list[Tensor], query: Tensor, eps: float, scale: float,
+                         save: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """The source-list forward launch; ``save`` as for ``packed_forward_impl``."""
     lib = _native.load()
     first = sources[0]
     query = _contiguous(query)
@@ -232,18 +265,25 @@ def sources_forward(sources: list[Tensor], query: Tensor, eps: float,
     device = first.device
     prepared, pointers, row_strides = _source_table(sources)
     out = torch.empty(first.shape, device=device, dtype=_BF16)
-    out_refine = torch.empty((tokens, width), device=device, dtype=torch.int8)
+    out_refine = torch.empty((tokens if save else 0, width), device=device, dtype=torch.int8)
     logit = torch.empty((tokens, count), device=device, dtype=_F32)
     inv_rms = torch.empty((tokens, count), device=device, dtype=_F32)
     stats = torch.empty((2, tokens), device=device, dtype=_F32)
     with torch.cuda.device(device):
         status = lib.attnres_hip_sources_forward(
             pointers, row_strides, count, tokens, width, query.data_ptr(), query.numel(),
-            eps, scale, out.data_ptr(), out_refine.data_ptr(), logit.data_ptr(),
+            eps, scale, out.data_ptr(), _pointer(out_refine), logit.data_ptr(),
             inv_rms.data_ptr(), stats.data_ptr(), _stream(device))
     del prepared  # copies (if any) stay alive until the launch is enqueued
     _native.check(status, "attnres source-list forward")
     return out, out_refine, logit, inv_rms, stats
+
+
+@torch.library.custom_op("attnres_hip::sources_forward", mutates_args=(),
+                         device_types="cuda", tags=_OP_TAGS)
+def sources_forward(sources: list[Tensor], query: Tensor, eps: float,
+                    scale: float) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    return sources_forward_impl(sources, query, eps, scale, saves_refinement(len(sources)))
 
 
 @sources_forward.register_fake
@@ -251,7 +291,7 @@ def _sources_forward_fake(sources, query, eps, scale):
     first = sources[0]
     count, tokens = len(sources), _rows_of(first.shape)
     return (first.new_empty(first.shape),
-            first.new_empty((tokens, int(first.shape[-1])), dtype=torch.int8),
+            first.new_empty((_refine_rows(count, tokens), int(first.shape[-1])), dtype=torch.int8),
             first.new_empty((tokens, count), dtype=_F32),
             first.new_empty((tokens, count), dtype=_F32),
             first.new_empty((2, tokens), dtype=_F32))
@@ -267,6 +307,7 @@ def sources_backward(sources: list[Tensor], query: Tensor, out: Tensor, out_refi
     query = _contiguous(query)
     out = _contiguous(out)
     grad_out = _contiguous(grad_out.to(_BF16))
+    recompute = out_refine.numel() == 0
     count, tokens, width = len(sources), _rows_of(first.shape), int(first.shape[-1])
     rank = query.numel()
     device = first.device
@@ -278,8 +319,8 @@ def sources_backward(sources: list[Tensor], query: Tensor, out: Tensor, out_refi
     with torch.cuda.device(device):
         status = lib.attnres_hip_sources_backward(
             pointers, row_strides, count, tokens, width, query.data_ptr(), rank, scale,
-            out.data_ptr(), _contiguous(out_refine).data_ptr(), grad_out.data_ptr(),
-            _contiguous(logit).data_ptr(),
+            None if recompute else out.data_ptr(), None if recompute else _contiguous(out_refine).data_ptr(),
+            grad_out.data_ptr(), _contiguous(logit).data_ptr(),
             _contiguous(inv_rms).data_ptr(), _contiguous(stats).data_ptr(), grad_pointers,
             grad_query.data_ptr(), workspace.data_ptr(), workspace.numel(), _stream(device))
     del prepared
@@ -299,7 +340,8 @@ def _sources_setup_context(ctx: Any, inputs: tuple, output: tuple) -> None:
     out, out_refine, logit, inv_rms, stats = output
     ctx.mark_non_differentiable(out_refine, logit, inv_rms, stats)
     ctx.set_materialize_grads(False)
-    ctx.save_for_backward(*sources, query, out, out_refine, logit, inv_rms, stats)
+    saved_out = out if out_refine.numel() else out_refine
+    ctx.save_for_backward(*sources, query, saved_out, out_refine, logit, inv_rms, stats)
     ctx.count = len(sources)
     ctx.scale = float(scale)
 
@@ -327,6 +369,7 @@ def sources_attnres(sources: tuple[Tensor, ...], query: Tensor, eps: float,
 
 
 __all__ = [
-    "packed_attnres", "packed_backward", "packed_forward", "prepare_rows", "row_stride",
-    "sources_attnres", "sources_backward", "sources_forward",
+    "RECOMPUTE_MAX_SOURCES", "packed_attnres", "packed_backward", "packed_forward", "packed_forward_impl",
+    "prepare_rows", "row_stride", "saves_refinement", "sources_attnres", "sources_backward", "sources_forward",
+    "sources_forward_impl",
 ]

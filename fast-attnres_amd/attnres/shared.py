@@ -39,7 +39,7 @@ import torch
 from torch import Tensor
 
 from . import _native
-from ._ops import _contiguous, _dq_workspace, _source_table, _stream, packed_forward, sources_forward
+from ._ops import _contiguous, _dq_workspace, _source_table, _stream, packed_forward_impl, sources_forward_impl
 from ._sources import _EPS, _MAX_SOURCES, _MAX_WIDTH, check_packed, check_sources
 
 
@@ -136,7 +136,8 @@ class _Read(torch.autograd.Function):
     @staticmethod
     def forward(ctx, bank: SharedSources, token: Tensor, query: Tensor, eps: float, scale: float) -> Tensor:
         query = _contiguous(query)
-        out, out_refine, logit, inv_rms, stats = sources_forward(list(bank.sources), query, eps, scale)
+        # always saved: the accumulating kernels read the refinement
+        out, out_refine, logit, inv_rms, stats = sources_forward_impl(list(bank.sources), query, eps, scale, True)
         ctx.bank = bank
         ctx.scale = scale
         ctx.token_device = token.device
@@ -270,7 +271,7 @@ class _BankRead(torch.autograd.Function):
         query = _contiguous(query)
         values = bank._values[:count]
         flat = values.reshape(count, -1, values.shape[-1])  # a view: the bank is contiguous
-        out, out_refine, logit, inv_rms, stats = packed_forward(flat, query, eps, scale)
+        out, out_refine, logit, inv_rms, stats = packed_forward_impl(flat, query, eps, scale, True)
         ctx.bank, ctx.count, ctx.scale = bank, count, scale
         ctx.token_device = tokens[0].device
         ctx.save_for_backward(query, out, out_refine, logit, inv_rms, stats)

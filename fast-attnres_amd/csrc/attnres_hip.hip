@@ -25,6 +25,7 @@ namespace attnres_hip {
 
 ATTNRES_FOR_EACH_GEOMETRY(ATTNRES_DECLARE_GEOMETRY)
 ATTNRES_FOR_EACH_GEOMETRY(ATTNRES_DECLARE_GEOMETRY_F32)
+ATTNRES_FOR_EACH_GEOMETRY(ATTNRES_DECLARE_GEOMETRY_RECOMPUTE)
 
 namespace {
 
@@ -140,20 +141,30 @@ int64_t launch_bwd_geometry_any(const BwdArgs<Rows, Grads>& a, bool nomask, bool
   }
 }
 
+// The recompute kernel (no saved refinement) exists for BF16 gradients only.
+template <int G, int CH, class Rows, class Grads>
+int64_t launch_bwd_select(const BwdArgs<Rows, Grads>& a, bool nomask, bool vec, bool acc, bool recompute,
+                          hipStream_t stream) {
+  if constexpr (!std::is_same_v<Grads, PackedGradsF32>) {
+    if (recompute) return launch_bwd_recompute_geometry<G, CH>(a, nomask, vec, stream);
+  }
+  return launch_bwd_geometry_any<G, CH>(a, nomask, vec, acc, stream);
+}
+
 template <class Rows, class Grads>
-int launch_backward(const BwdArgs<Rows, Grads>& a, bool vec, bool acc, float* slices, float* dq32, uint16_t* dq16,
-                    hipStream_t stream) {
+int launch_backward(const BwdArgs<Rows, Grads>& a, bool vec, bool acc, bool recompute, float* slices, float* dq32,
+                    uint16_t* dq16, hipStream_t stream) {
   const Geometry geo = geometry(a.width);
   const bool nomask = no_mask(geo, a.width, a.rank);
   int64_t blocks = 0;
   switch (geo.lanes * 100 + geo.chunks) {
-    case 1601: blocks = launch_bwd_geometry_any<16, 1>(a, nomask, vec, acc, stream); break;
-    case 3201: blocks = launch_bwd_geometry_any<32, 1>(a, nomask, vec, acc, stream); break;
-    case 6401: blocks = launch_bwd_geometry_any<64, 1>(a, nomask, vec, acc, stream); break;
-    case 6402: blocks = launch_bwd_geometry_any<64, 2>(a, nomask, vec, acc, stream); break;
-    case 6404: blocks = launch_bwd_geometry_any<64, 4>(a, nomask, vec, acc, stream); break;
-    case 6408: blocks = launch_bwd_geometry_any<64, 8>(a, nomask, vec, acc, stream); break;
-    default: blocks = launch_bwd_geometry_any<256, 4>(a, nomask, vec, acc, stream); break;
+    case 1601: blocks = launch_bwd_select<16, 1>(a, nomask, vec, acc, recompute, stream); break;
+    case 3201: blocks = launch_bwd_select<32, 1>(a, nomask, vec, acc, recompute, stream); break;
+    case 6401: blocks = launch_bwd_select<64, 1>(a, nomask, vec, acc, recompute, stream); break;
+    case 6402: blocks = launch_bwd_select<64, 2>(a, nomask, vec, acc, recompute, stream); break;
+    case 6404: blocks = launch_bwd_select<64, 4>(a, nomask, vec, acc, recompute, stream); break;
+    case 6408: blocks = launch_bwd_select<64, 8>(a, nomask, vec, acc, recompute, stream); break;
+    default: blocks = launch_bwd_select<256, 4>(a, nomask, vec, acc, recompute, stream); break;
   }
   int st = launch_status("attnres backward");
   if (st != ATTNRES_OK) return st;
@@ -189,6 +200,17 @@ bool set_accumulate(BwdArgs<Rows, Grads>& a, const uint8_t* flags, int64_t n_sou
   return any;
 }
 
+// The pointer is 16-byte aligned or absent.
+bool aligned16_or_null(const void* p) { return !p || aligned16(p); }
+
+// Backward without the saved output: the recompute kernel, for small reads only.
+int check_recompute(bool recompute, int64_t S, const char* name) {
+  if (recompute && S > kRecomputeMaxSources)
+    return fail(ATTNRES_ERR_SHAPE, "%s without out_refine needs n_sources <= %d (got %lld)", name,
+                kRecomputeMaxSources, (long long)S);
+  return ATTNRES_OK;
+}
+
 // Workspace layout (FP32): [max_blocks, R] partial rows, [slices, R], [R] total.
 int64_t workspace_elems(int64_t N, int64_t D, int64_t R) {
   const int64_t rows = grid_blocks(N, D, 0);
@@ -208,6 +230,8 @@ const char* attnres_hip_version(void) { return "2.0.0"; }
 
 const char* attnres_hip_last_error(void) { return g_error; }
 
+int attnres_hip_saves_refinement(int64_t n_sources) { return n_sources > kRecomputeMaxSources ? 1 : 0; }
+
 int64_t attnres_hip_dq_workspace_elems(int64_t n_tokens, int64_t width, int64_t rank) {
   if (check_shape(1, n_tokens, width, rank) != ATTNRES_OK) return -1;
   return workspace_elems(n_tokens, width, rank);
@@ -220,7 +244,7 @@ int attnres_hip_packed_forward(const void* values, int64_t source_stride, int64_
                                float* stats, void* stream) {
   int st = check_shape(n_sources, n_tokens, width, rank);
   if (st) return st;
-  if (!values || !query || !out || !out_refine || !logit || !inv_rms || !stats)
+  if (!values || !query || !out || !logit || !inv_rms || !stats)
     return fail(ATTNRES_ERR_NULL_POINTER, "null pointer argument to attnres_hip_packed_forward");
   if (source_stride < 0 || row_stride < 0) return fail(ATTNRES_ERR_STRIDE, "negative stride");
   if ((st = check_scalars(eps, scale, true))) return st;
@@ -238,7 +262,7 @@ int attnres_hip_packed_forward(const void* values, int64_t source_stride, int64_
   a.rank = static_cast<int>(rank);
   a.eps = eps;
   a.scale = scale;
-  const bool vec = width % kVec == 0 && aligned16(values) && aligned16(out) && aligned16(out_refine) &&
+  const bool vec = width % kVec == 0 && aligned16(values) && aligned16(out) && aligned16_or_null(out_refine) &&
                    (source_stride % kVec == 0 || n_sources == 1) && (row_stride % kVec == 0 || n_tokens == 1);
   return launch_forward(a, vec, static_cast<hipStream_t>(stream));
 }
@@ -260,9 +284,11 @@ int packed_backward(const void* values, int64_t source_stride, int64_t row_strid
                      : need_flags ? "attnres_hip_packed_backward_accumulate" : "attnres_hip_packed_backward";
   int st = check_shape(n_sources, n_tokens, width, rank);
   if (st) return st;
-  if (!values || !query || !out || !out_refine || !grad_out || !logit || !inv_rms || !stats ||
+  const bool recompute = !need_flags && !out_refine;
+  if (!values || !query || (!recompute && (!out || !out_refine)) || !grad_out || !logit || !inv_rms || !stats ||
       !grad_values || !grad_query || !dq_workspace || (need_flags && !accumulate))
     return fail(ATTNRES_ERR_NULL_POINTER, "null pointer argument to %s", name);
+  if ((st = check_recompute(recompute, n_sources, name))) return st;
   if (source_stride < 0 || row_stride < 0) return fail(ATTNRES_ERR_STRIDE, "negative stride");
   if ((st = check_scalars(1.0f, scale, false))) return st;
   const int64_t need = workspace_elems(n_tokens, width, rank);
@@ -289,14 +315,14 @@ int packed_backward(const void* values, int64_t source_stride, int64_t row_strid
   a.width = static_cast<int>(width);
   a.rank = static_cast<int>(rank);
   a.scale = scale;
-  const bool vec = width % kVec == 0 && aligned16(values) && aligned16(out) && aligned16(out_refine) &&
-                   aligned16(grad_out) && aligned16(grad_values) &&
+  const bool vec = width % kVec == 0 && aligned16(values) && aligned16_or_null(out) &&
+                   aligned16_or_null(out_refine) && aligned16(grad_out) && aligned16(grad_values) &&
                    (source_stride % kVec == 0 || n_sources == 1) && (row_stride % kVec == 0 || n_tokens == 1);
   const bool acc = set_accumulate(a, accumulate, n_sources);
   const int64_t rows = grid_blocks(n_tokens, width, 0);
   float* slices = dq_workspace + rows * rank;
   float* dq32 = dq_workspace + (need - rank);
-  return launch_backward(a, vec, acc, slices, dq32, static_cast<uint16_t*>(grad_query),
+  return launch_backward(a, vec, acc, recompute, slices, dq32, static_cast<uint16_t*>(grad_query),
                          static_cast<hipStream_t>(stream));
 }
 
@@ -350,11 +376,11 @@ int attnres_hip_sources_forward(const void* const* sources, const int64_t* row_s
                                 void* stream) {
   int st = check_shape(n_sources, n_tokens, width, rank);
   if (st) return st;
-  if (!sources || !row_strides || !query || !out || !out_refine || !logit || !inv_rms || !stats)
+  if (!sources || !row_strides || !query || !out || !logit || !inv_rms || !stats)
     return fail(ATTNRES_ERR_NULL_POINTER, "null pointer argument to attnres_hip_sources_forward");
   if ((st = check_scalars(eps, scale, true))) return st;
   FwdArgs<ListRows> a{};
-  bool vec = width % kVec == 0 && aligned16(out) && aligned16(out_refine);
+  bool vec = width % kVec == 0 && aligned16(out) && aligned16_or_null(out_refine);
   for (int64_t s = 0; s < n_sources; ++s) {
     if (!sources[s]) return fail(ATTNRES_ERR_NULL_POINTER, "source %lld is null", (long long)s);
     if (row_strides[s] < 0) return fail(ATTNRES_ERR_STRIDE, "source %lld has a negative row stride", (long long)s);
@@ -391,16 +417,18 @@ int sources_backward(const void* const* sources, const int64_t* row_strides, int
   const char* name = need_flags ? "attnres_hip_sources_backward_accumulate" : "attnres_hip_sources_backward";
   int st = check_shape(n_sources, n_tokens, width, rank);
   if (st) return st;
-  if (!sources || !row_strides || !query || !out || !out_refine || !grad_out || !logit ||
+  const bool recompute = !need_flags && !out_refine;
+  if (!sources || !row_strides || !query || (!recompute && (!out || !out_refine)) || !grad_out || !logit ||
       !inv_rms || !stats || !grad_sources || !grad_query || !dq_workspace || (need_flags && !accumulate))
     return fail(ATTNRES_ERR_NULL_POINTER, "null pointer argument to %s", name);
+  if ((st = check_recompute(recompute, n_sources, name))) return st;
   if ((st = check_scalars(1.0f, scale, false))) return st;
   const int64_t need = workspace_elems(n_tokens, width, rank);
   if (dq_workspace_elems < need)
     return fail(ATTNRES_ERR_WORKSPACE, "dq workspace has %lld elements, needs %lld",
                 (long long)dq_workspace_elems, (long long)need);
   BwdArgs<ListRows, ListGrads> a{};
-  bool vec = width % kVec == 0 && aligned16(out) && aligned16(out_refine) && aligned16(grad_out);
+  bool vec = width % kVec == 0 && aligned16_or_null(out) && aligned16_or_null(out_refine) && aligned16(grad_out);
   for (int64_t s = 0; s < n_sources; ++s) {
     if (!sources[s] || !grad_sources[s])
       return fail(ATTNRES_ERR_NULL_POINTER, "source %lld or its gradient is null", (long long)s);
@@ -428,7 +456,7 @@ int sources_backward(const void* const* sources, const int64_t* row_strides, int
   const int64_t rows = grid_blocks(n_tokens, width, 0);
   float* slices = dq_workspace + rows * rank;
   float* dq32 = dq_workspace + (need - rank);
-  return launch_backward(a, vec, acc, slices, dq32, static_cast<uint16_t*>(grad_query),
+  return launch_backward(a, vec, acc, recompute, slices, dq32, static_cast<uint16_t*>(grad_query),
                          static_cast<hipStream_t>(stream));
 }
 

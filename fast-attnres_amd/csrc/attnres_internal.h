@@ -22,6 +22,9 @@ constexpr int kBlock = 256;           // threads per workgroup (4 wavefronts)
 constexpr int kVec = 8;               // BF16 elements per chunk (16 bytes)
 constexpr int kMaxGridBlocks = 2048;  // persistent grid cap
 constexpr int kFinalizeSlices = 64;   // first-stage slices of the dq reduction
+// Save/recompute policy: reads of at most this many sources save no output
+// refinement; their backward derives delta from the value rows.
+constexpr int kRecomputeMaxSources = ATTNRES_RECOMPUTE_MAX_SOURCES;
 
 // ---------------------------------------------------------------- addressing
 
@@ -76,7 +79,7 @@ struct FwdArgs {
   Rows src;
   const uint16_t* query;  // [R] BF16, contiguous
   uint16_t* out;          // [N, D] BF16, contiguous
-  int8_t* out_refine;     // [N, D] low-order correction of out
+  int8_t* out_refine;     // [N, D] low-order correction of out; nullptr: not stored
   float* logit;           // [N, S]
   float* inv_rms;         // [N, S]
   float* stats;           // [2, N]
@@ -93,8 +96,8 @@ struct BwdArgs {
   Rows src;
   Grads grad;
   const uint16_t* query;
-  const uint16_t* out;       // [N, D] BF16 forward output, contiguous
-  const int8_t* out_refine;  // [N, D] its low-order correction
+  const uint16_t* out;       // [N, D] BF16 forward output, contiguous (unused by the recompute kernel)
+  const int8_t* out_refine;  // [N, D] its low-order correction (likewise)
   const uint16_t* grad_out;  // [N, D] BF16, contiguous
   const float* logit;
   const float* inv_rms;
@@ -166,6 +169,17 @@ int64_t launch_bwd_geometry(const BwdArgs<Rows, Grads>& a, bool nomask, bool vec
       const BwdArgs<PackedRows, PackedGrads>&, bool, bool, bool, hipStream_t);                           \
   extern template int64_t launch_bwd_geometry<G, CH, ListRows, ListGrads>(                               \
       const BwdArgs<ListRows, ListGrads>&, bool, bool, bool, hipStream_t);
+
+// Enqueue the recompute-policy backward (n_sources <= kRecomputeMaxSources;
+// reads no saved output or refinement); returns the grid size.
+template <int G, int CH, class Rows, class Grads>
+int64_t launch_bwd_recompute_geometry(const BwdArgs<Rows, Grads>& a, bool nomask, bool vec, hipStream_t stream);
+
+#define ATTNRES_DECLARE_GEOMETRY_RECOMPUTE(G, CH)                                               \
+  extern template int64_t launch_bwd_recompute_geometry<G, CH, PackedRows, PackedGrads>(        \
+      const BwdArgs<PackedRows, PackedGrads>&, bool, bool, hipStream_t);                        \
+  extern template int64_t launch_bwd_recompute_geometry<G, CH, ListRows, ListGrads>(            \
+      const BwdArgs<ListRows, ListGrads>&, bool, bool, hipStream_t);
 
 // The accumulating backward into FP32 gradient sums (packed sources only).
 template <int G, int CH>

@@ -143,8 +143,8 @@ __device__ __forceinline__ int refine_encode(float o, uint32_t bf16_bits) {
   return (e >= 16 && e <= 254) ? static_cast<int>(t) : 0;
 }
 
-// Store this lane's chunks of a BF16 row and of its refinement bytes.
-template <int G, int CH, bool NOMASK, bool VEC>
+// Store this lane's chunks of a BF16 row and (REFINE) of its refinement bytes.
+template <int G, int CH, bool NOMASK, bool VEC, bool REFINE>
 __device__ __forceinline__ void store_row_refined(uint16_t* __restrict__ row, int8_t* __restrict__ refine,
                                                   int lane, int D, const float (&x)[CH][kVec]) {
 #pragma unroll
@@ -156,12 +156,15 @@ __device__ __forceinline__ void store_row_refined(uint16_t* __restrict__ row, in
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       w[j] = pack_bf16x2(x[c][2 * j], x[c][2 * j + 1]);
-      const uint32_t q0 = static_cast<uint32_t>(refine_encode(x[c][2 * j], w[j] & 0xffffu)) & 0xffu;
-      const uint32_t q1 = static_cast<uint32_t>(refine_encode(x[c][2 * j + 1], w[j] >> 16)) & 0xffu;
-      r[j >> 1] |= (q0 | (q1 << 8)) << (16 * (j & 1));
+      if constexpr (REFINE) {
+        const uint32_t q0 = static_cast<uint32_t>(refine_encode(x[c][2 * j], w[j] & 0xffffu)) & 0xffu;
+        const uint32_t q1 = static_cast<uint32_t>(refine_encode(x[c][2 * j + 1], w[j] >> 16)) & 0xffu;
+        r[j >> 1] |= (q0 | (q1 << 8)) << (16 * (j & 1));
+      }
     }
     store_chunk<VEC>(row, d0, D, u32x4{w[0], w[1], w[2], w[3]});
-    if constexpr (VEC) {
+    if constexpr (!REFINE) {
+    } else if constexpr (VEC) {
       __builtin_nontemporal_store(u32x2{r[0], r[1]}, reinterpret_cast<u32x2*>(refine + d0));
     } else {
 #pragma unroll
@@ -340,8 +343,8 @@ __device__ __forceinline__ void refill(const Rows& src, const ItemCursor& at, bo
 // coordinate and no word masks are needed.
 //
 // Group g takes tokens g, g + groups, ... and streams their rows through the
-// ring without draining it between tokens (launched with one token per group,
-// see launch_fwd).
+// ring without draining it between tokens (launched with a persistent grid
+// for small S, else with one token per group; see launch_fwd).
 template <int G, int CH, int NB, bool NOMASK, bool VEC, class Rows>
 __global__ void __launch_bounds__(kBlock) attnres_fwd_kernel(const FwdArgs<Rows> a) {
   static_assert(G <= 64 || G == kBlock, "a wide group is the whole workgroup");
@@ -474,7 +477,13 @@ __global__ void __launch_bounds__(kBlock) attnres_fwd_kernel(const FwdArgs<Rows>
       for (int c = 0; c < CH; ++c)
 #pragma unroll
         for (int e = 0; e < kVec; ++e) acc[c][e] *= inv_sum;
-      store_row_refined<G, CH, NOMASK, VEC>(a.out + token * D, a.out_refine + token * D, lane, D, acc);
+      // No refinement under the recompute policy (out_refine == nullptr, a
+      // kernel argument: the branch is uniform over the grid).
+      if (a.out_refine) {
+        store_row_refined<G, CH, NOMASK, VEC, true>(a.out + token * D, a.out_refine + token * D, lane, D, acc);
+      } else {
+        store_row_refined<G, CH, NOMASK, VEC, false>(a.out + token * D, nullptr, lane, D, acc);
+      }
       if (lane == 0) {
         a.stats[token] = run_max;
         a.stats[a.n_tokens + token] = inv_sum;
@@ -581,13 +590,40 @@ __device__ __forceinline__ float token_delta(const TokenRows<CH>& t) {
   return (m0 + m1) + corr;
 }
 
-// Persistent: group g takes tokens g, g + groups, ..., and the value rows
-// stream through the ring across token boundaries.  The next token's dO,
-// output, refinement bytes and statistics
-// are requested `lead` = min(NB, S) items before the current token ends,
-// right after a ring refill, and folded into delta on the token's last item
-// -- when the younger rows in the ring are still in flight -- so a token
-// switch does not drain the ring.
+// The query on this workgroup's row positions, FP32, +0 off the key (every
+// group of the workgroup reads it from LDS).  Ends with a barrier.
+template <int G, int CH>
+__device__ __forceinline__ void fill_query_lds(const uint16_t* __restrict__ query, float* q_lds, int tail0, int D,
+                                               int R) {
+  for (int d = threadIdx.x; d < G * CH * kVec; d += kBlock) {
+    const uint32_t bits = query[min(max(d - tail0, 0), R - 1)];
+    q_lds[d] = (d >= tail0 && d < D) ? __uint_as_float(bits << 16) : 0.0f;
+  }
+  __syncthreads();
+}
+
+// Fixed-order reduction of the groups' dq into this block's partial row
+// (`dq_lds` holds kBlock * kVec floats).  Every thread of the block calls it.
+template <int G, int CH>
+__device__ __forceinline__ void store_dq_partial(const float (&dq)[CH][kVec], float* dq_lds, float* partial,
+                                                 int group, int lane, int tail0, int D) {
+  constexpr int kGroups = kBlock / G;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) dq_lds[group * (G * kVec) + lane * kVec + e] = dq[c][e];
+    __syncthreads();
+    for (int j = threadIdx.x; j < G * kVec; j += kBlock) {
+      float t = dq_lds[j];
+#pragma unroll
+      for (int k = 1; k < kGroups; ++k) t += dq_lds[k * (G * kVec) + j];
+      const int d = c * G * kVec + j;
+      if (d >= tail0 && d < D) partial[d - tail0] = t;
+    }
+    __syncthreads();
+  }
+}
+
 // One FP32 row (this lane's chunks, two 16-byte words each), unconditional
 // like load_row: chunks at or beyond D read the row start (VEC) or clamped
 // elements.  VEC requires 16-byte aligned rows and D % 8 == 0.
@@ -619,6 +655,13 @@ struct GradRows {
   __device__ __forceinline__ const uint16_t* row(int s, int64_t n) const { return grad.row(s, n, width); }
 };
 
+// Persistent: group g takes tokens g, g + groups, ..., and the value rows
+// stream through the ring across token boundaries.  The next token's dO,
+// output, refinement bytes and statistics are requested `lead` = min(NB, S)
+// items before the current token ends, right after a ring refill, and folded
+// into delta on the token's last item -- when the younger rows in the ring
+// are still in flight -- so a token switch does not drain the ring.
+//
 // ACC: the accumulating variant.  For a source whose bit is set in
 // a.accumulate, the item's gradient row is prefetched with its value row (a
 // second ring; other items load the idle row, so every load stays
@@ -646,11 +689,7 @@ __global__ void __launch_bounds__(kBlock) attnres_bwd_kernel(const BwdArgs<Rows,
   const float scale = a.scale;
   int phase = 0;
 
-  for (int d = threadIdx.x; d < G * CH * kVec; d += kBlock) {
-    const uint32_t bits = a.query[min(max(d - tail0, 0), R - 1)];
-    q_lds[d] = (d >= tail0 && d < D) ? __uint_as_float(bits << 16) : 0.0f;
-  }
-  __syncthreads();
+  fill_query_lds<G, CH>(a.query, q_lds, tail0, D, R);
   uint32_t km[CH][4];
   if constexpr (!NOMASK) key_masks<G, CH>(lane, D, tail0, km);
   float dq[CH][kVec];
@@ -833,22 +872,124 @@ __global__ void __launch_bounds__(kBlock) attnres_bwd_kernel(const BwdArgs<Rows,
     }
   }
 
-  // Fixed-order reduction of the groups' dq into this block's partial row.
-  float* partial = a.partial + static_cast<int64_t>(blockIdx.x) * R;
+  store_dq_partial<G, CH>(dq, dq_lds, a.partial + static_cast<int64_t>(blockIdx.x) * R, group, lane, tail0, D);
+}
+
+// ------------------------------------------------ backward, recompute policy
+
+// For S <= kRecomputeMaxSources the forward stores no refinement and this
+// backward reads neither the output nor its refinement: a group holds every
+// value row of its token at once, and delta = <dO, o> = sum_s p_s <v_s, dO>
+// comes from the dw_s = <v_s, dO> it needs anyway (o = sum_s p_s v_s),
+// summed in source order.  Grid-stride over tokens on the persistent grid;
+// the S + 1 rows of a token are requested together and occupancy hides
+// their latency.  Rows s >= S re-read row 0 (cached) and are not used.
+template <int G, int CH, bool NOMASK, bool VEC, class Rows, class Grads>
+__global__ void __launch_bounds__(kBlock) attnres_bwd_recompute_kernel(const BwdArgs<Rows, Grads> a) {
+  constexpr int SM = kRecomputeMaxSources;
+  static_assert(G <= 64 || G == kBlock, "a wide group is the whole workgroup");
+  constexpr int kGroups = kBlock / G;
+  __shared__ float xred[xred_floats<G>(SM)];
+  __shared__ float dq_lds[kGroups * G * kVec];
+  __shared__ __attribute__((aligned(16))) float q_lds[G * CH * kVec];
+  const int lane = threadIdx.x % G;
+  const int group = group_index<G>();
+  const int D = a.width;
+  const int R = a.rank;
+  const int tail0 = D - R;
+  const int S = a.n_sources;
+  const float inv_R = 1.0f / static_cast<float>(R);
+  const float scale = a.scale;
+  int phase = 0;
+
+  fill_query_lds<G, CH>(a.query, q_lds, tail0, D, R);
+  uint32_t km[CH][4];
+  if constexpr (!NOMASK) key_masks<G, CH>(lane, D, tail0, km);
+  float dq[CH][kVec];
 #pragma unroll
-  for (int c = 0; c < CH; ++c) {
+  for (int c = 0; c < CH; ++c)
 #pragma unroll
-    for (int e = 0; e < kVec; ++e) dq_lds[group * (G * kVec) + lane * kVec + e] = dq[c][e];
-    __syncthreads();
-    for (int j = threadIdx.x; j < G * kVec; j += kBlock) {
-      float t = dq_lds[j];
+    for (int e = 0; e < kVec; ++e) dq[c][e] = 0.0f;
+
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * kGroups + group;
+  const int64_t groups = static_cast<int64_t>(gridDim.x) * kGroups;
+  const int64_t my_tokens = gid < a.n_tokens ? (a.n_tokens - 1 - gid) / groups + 1 : 0;
+  for (int64_t i = 0; i < my_tokens; ++i) {
+    const int64_t token = gid + i * groups;
+    u32x4 g[CH];
+    u32x4 v[SM][CH];
+    load_row<G, CH, VEC>(a.grad_out + token * D, lane, D, g);
 #pragma unroll
-      for (int k = 1; k < kGroups; ++k) t += dq_lds[k * (G * kVec) + j];
-      const int d = c * G * kVec + j;
-      if (d >= tail0 && d < D) partial[d - tail0] = t;
+    for (int s = 0; s < SM; ++s) load_row<G, CH, VEC>(a.src.row(s < S ? s : 0, token), lane, D, v[s]);
+    float z[SM], ir[SM];
+#pragma unroll
+    for (int s = 0; s < SM; ++s) {
+      const int64_t item = token * S + (s < S ? s : 0);
+      z[s] = a.logit[item];
+      ir[s] = a.inv_rms[item];
     }
-    __syncthreads();
+    const float run_max = a.stats[token];
+    const float inv_sum = a.stats[a.n_tokens + token];
+    if constexpr (!NOMASK) mask_range<G, CH>(lane, D, g);
+
+    float dw[SM];
+#pragma unroll
+    for (int s = 0; s < SM; ++s) {
+      float d0 = 0.0f, d1 = 0.0f;
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        d0 = dot2(v[s][c].x, g[c].x, d0);
+        d1 = dot2(v[s][c].y, g[c].y, d1);
+        d0 = dot2(v[s][c].z, g[c].z, d0);
+        d1 = dot2(v[s][c].w, g[c].w, d1);
+      }
+      dw[s] = d0 + d1;
+    }
+    group_sum<G, SM>(dw, xred, phase);
+    float p[SM];
+    float delta = 0.0f;
+#pragma unroll
+    for (int s = 0; s < SM; ++s) {
+      p[s] = __expf(z[s] - run_max) * inv_sum;
+      delta = s < S ? fmaf(p[s], dw[s], delta) : delta;
+    }
+
+#pragma unroll
+    for (int s = 0; s < SM; ++s) {
+      if (s >= S) break;  // uniform
+      const float dz = p[s] * (dw[s] - delta);
+      const float ca = ir[s] * (dz * scale);                    // on q; dq += ca * key
+      const float cb = -(ir[s] * ir[s]) * (dz * z[s] * inv_R);  // on the key coordinates
+      uint16_t* grad_row = a.grad.row(s, token, D);
+      // dO unpacked per source (see the streaming kernel: a hoisted unpacked
+      // copy would cost CH * 8 registers).
+      const uint32_t lo_shift = 16u | (static_cast<uint32_t>(s + S) >> 31);
+      const uint32_t hi_mask = 0xffff0000u | (static_cast<uint32_t>(s + S) >> 31);
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const int d0 = chunk_start<G>(c, lane);
+        const uint32_t w[4] = {v[s][c].x, v[s][c].y, v[s][c].z, v[s][c].w};
+        const uint32_t gw[4] = {g[c].x, g[c].y, g[c].z, g[c].w};
+        const float4 qa = *reinterpret_cast<const float4*>(&q_lds[d0]);
+        const float4 qb = *reinterpret_cast<const float4*>(&q_lds[d0 + 4]);
+        const float qf[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+        uint32_t out[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t kw = NOMASK ? w[k] : (w[k] & km[c][k]);
+          const float k0 = bf16_lo(kw), k1 = bf16_hi(kw);
+          const float g0 = __uint_as_float(gw[k] << lo_shift), g1 = __uint_as_float(gw[k] & hi_mask);
+          const float v0 = fmaf(cb, k0, fmaf(ca, qf[2 * k], p[s] * g0));
+          const float v1 = fmaf(cb, k1, fmaf(ca, qf[2 * k + 1], p[s] * g1));
+          dq[c][2 * k] = fmaf(ca, k0, dq[c][2 * k]);
+          dq[c][2 * k + 1] = fmaf(ca, k1, dq[c][2 * k + 1]);
+          out[k] = pack_bf16x2(v0, v1);
+        }
+        if (NOMASK || d0 < D) store_chunk<VEC>(grad_row, d0, D, u32x4{out[0], out[1], out[2], out[3]});
+      }
+    }
   }
+  store_dq_partial<G, CH>(dq, dq_lds, a.partial + static_cast<int64_t>(blockIdx.x) * R, group, lane, tail0, D);
 }
 
 // ----------------------------------------------------------------- launchers
@@ -884,13 +1025,27 @@ int64_t resident_blocks() {
   return cached;
 }
 
-// One token per group: workgroups that start as others retire spread the
-// output stores over time (a persistent grid, whose groups all finish a token
-// at once, measured 5% slower).
+// Grid shape of the forward.  Many sources: one token per group --
+// workgroups that start as others retire spread the output stores over time
+// (a persistent grid, whose groups all finish a token at once, is 2-6%
+// slower from S ~ 17 on).  Few sources: a persistent grid, whose groups
+// stream the rows of consecutive tokens through the ring without draining it
+// -- one token per group leaves a group only S rows to keep in flight before
+// it retires.  Measured on MI355X at N = 16384 (8192 for D = 8192), forward
+// time one token per group -> persistent: S = 1: 28 -> 26 us (D = 1024),
+// 59 -> 40 (2048), 144 -> 72 (4096), 110 -> 68 (8192); S = 5: 52 -> 46 (1024),
+// 98 -> 83 (2048), 227 -> 155 (4096); S = 9: 132 -> 126 (2048), 293 -> 241
+// (4096), 262 -> 249 (8192); S = 13 at D = 2048: equal; S = 17: 216 -> 224.
+constexpr int kPersistentFwdMaxSources = 12;
+
 template <int G, int CH, bool NOMASK, bool VEC, class Rows>
 void launch_fwd(const FwdArgs<Rows>& a, hipStream_t stream) {
   constexpr int64_t kGroups = kBlock / G;
-  const int64_t blocks = (a.n_tokens + kGroups - 1) / kGroups;
+  int64_t blocks = (a.n_tokens + kGroups - 1) / kGroups;
+  if (a.n_sources <= kPersistentFwdMaxSources) {
+    blocks = grid_blocks(a.n_tokens, a.width,
+                         resident_blocks<&attnres_fwd_kernel<G, CH, fwd_ring<CH>(), NOMASK, VEC, Rows>>());
+  }
   hipLaunchKernelGGL((attnres_fwd_kernel<G, CH, fwd_ring<CH>(), NOMASK, VEC, Rows>),
                      dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream, a);
 }
@@ -928,6 +1083,32 @@ int64_t launch_bwd_geometry(const BwdArgs<Rows, Grads>& a, bool nomask, bool vec
              : launch_bwd_variant<G, CH, false>(a, nomask, vec, stream);
 }
 
+template <int G, int CH, bool NOMASK, bool VEC, class Rows, class Grads>
+int64_t launch_bwd_recompute(const BwdArgs<Rows, Grads>& a, hipStream_t stream) {
+  const int64_t resident = resident_blocks<&attnres_bwd_recompute_kernel<G, CH, NOMASK, VEC, Rows, Grads>>();
+  const int64_t blocks = grid_blocks(a.n_tokens, a.width, resident);
+  hipLaunchKernelGGL((attnres_bwd_recompute_kernel<G, CH, NOMASK, VEC, Rows, Grads>),
+                     dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream, a);
+  return blocks;
+}
+
+// The recompute kernel keeps S rows per lane: for the (64, 8) geometry
+// (2048 < D <= 4096) it runs with a whole workgroup per token instead, two
+// chunks per lane (same lane positions covered, so the same NOMASK rule).
+template <int G, int CH, class Rows, class Grads>
+int64_t launch_bwd_recompute_geometry(const BwdArgs<Rows, Grads>& a, bool nomask, bool vec, hipStream_t stream) {
+  constexpr bool kWide = G == 64 && CH == 8;
+  constexpr int RG = kWide ? kBlock : G;
+  constexpr int RCH = kWide ? 2 : CH;
+  static_assert(RG * RCH == G * CH, "same row coverage");
+  if (nomask) {
+    return vec ? launch_bwd_recompute<RG, RCH, true, true>(a, stream)
+               : launch_bwd_recompute<RG, RCH, true, false>(a, stream);
+  }
+  return vec ? launch_bwd_recompute<RG, RCH, false, true>(a, stream)
+             : launch_bwd_recompute<RG, RCH, false, false>(a, stream);
+}
+
 template <int G, int CH>
 int64_t launch_bwd_geometry_f32(const BwdArgs<PackedRows, PackedGradsF32>& a, bool nomask, bool vec,
                                 hipStream_t stream) {
@@ -945,6 +1126,10 @@ template int64_t launch_bwd_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, ListRows, Li
     const BwdArgs<ListRows, ListGrads>&, bool, bool, bool, hipStream_t);
 template int64_t launch_bwd_geometry_f32<ATTNRES_LANES, ATTNRES_CHUNKS>(const BwdArgs<PackedRows, PackedGradsF32>&,
                                                                         bool, bool, hipStream_t);
+template int64_t launch_bwd_recompute_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, PackedRows, PackedGrads>(
+    const BwdArgs<PackedRows, PackedGrads>&, bool, bool, hipStream_t);
+template int64_t launch_bwd_recompute_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, ListRows, ListGrads>(
+    const BwdArgs<ListRows, ListGrads>&, bool, bool, hipStream_t);
 #else
 #error "compile attnres_kernels.hip with -DATTNRES_LANES=<G> -DATTNRES_CHUNKS=<CH>"
 #endif

@@ -35,6 +35,14 @@
  *   stats[2, N]   FP32, row 0 = max_s z_s, row 1 = 1/sum_s exp(z_s - max)
  * The two softmax statistics are kept separate on purpose: a single FP32
  * log-sum-exp loses the normaliser when logits share an offset near 2^24.
+ *
+ * Save/recompute policy.  A read of at most ATTNRES_RECOMPUTE_MAX_SOURCES
+ * sources need not save the output's refinement: pass out_refine = NULL to
+ * the forward (nothing is stored) and out = out_refine = NULL to the plain
+ * backward, which then derives delta = <dO, o> = sum_s p_s <v_s, dO> from
+ * the value rows it reads anyway.  Larger reads must save it.  (The reference
+ * makes the same structural choice: recompute for S <= 3, save the FP32
+ * mixed output for S >= 4, src/attnres/_kernels/fla_full_sources.py:146-161.)
  */
 #ifndef ATTNRES_HIP_H
 #define ATTNRES_HIP_H
@@ -58,6 +66,8 @@ enum attnres_status {
 /* Envelope (the reference's package limits, src/attnres/_sources.py:12-13). */
 #define ATTNRES_MAX_SOURCES 129
 #define ATTNRES_MAX_WIDTH 8192
+/* Reads of at most this many sources may skip the refinement (see above). */
+#define ATTNRES_RECOMPUTE_MAX_SOURCES 3
 
 /* Library version string, e.g. "1.0.0". */
 const char* attnres_hip_version(void);
@@ -66,9 +76,17 @@ const char* attnres_hip_version(void);
 const char* attnres_hip_last_error(void);
 
 /*
+ * The library's save/recompute policy for a read of n_sources sources:
+ * 1 = save (the forward stores out_refine, the backward reads out and
+ * out_refine), 0 = recompute (n_sources <= ATTNRES_RECOMPUTE_MAX_SOURCES).
+ * Host-only.  Replaces `_should_save_mixed` (fla_full_sources.py:146-161).
+ */
+int attnres_hip_saves_refinement(int64_t n_sources);
+
+/*
  * Packed forward.  values[s, n, :] lives at values + s*source_stride +
  * n*row_stride.  Writes out[N, D] (contiguous BF16), out_refine[N, D]
- * (contiguous int8) and the saved statistics.
+ * (contiguous int8; NULL: not stored) and the saved statistics.
  *
  * Replaces the launch inside the reference op
  * `attnres::_fixed_tail_forward_with_aux` (src/attnres/_kernels/fixed_tail.py:904-960),
@@ -96,7 +114,9 @@ int64_t attnres_hip_dq_workspace_elems(int64_t n_tokens, int64_t width,
  * out[N, D] and out_refine[N, D] (contiguous), grad_out[N, D] (contiguous
  * BF16) and the saved statistics; writes grad_values[S, N, D] (contiguous BF16) and
  * grad_query[R] (BF16).  dq is reduced over all tokens in a fixed order, so it
- * is bit-identical from run to run.
+ * is bit-identical from run to run.  out_refine = NULL (and out ignored, may
+ * be NULL) selects the recompute kernel: n_sources must then be at most
+ * ATTNRES_RECOMPUTE_MAX_SOURCES (else ATTNRES_ERR_SHAPE).
  *
  * Replaces `attnres::_fixed_tail_backward` (fixed_tail.py:962-1034):
  * `_packed_online_backward_kernel` (fixed_tail.py:485-873) plus
@@ -117,7 +137,8 @@ int attnres_hip_packed_backward(const void* values, int64_t source_stride,
 /*
  * Source-list forward.  `sources` and `row_strides` are HOST arrays of
  * n_sources entries: source s, row n starts at sources[s] + n*row_strides[s].
- * Sources are never packed or copied.  Same outputs as the packed forward.
+ * Sources are never packed or copied.  Same outputs as the packed forward
+ * (out_refine may be NULL likewise).
  *
  * Replaces `attnres::_fixed_tail_sources_forward_with_aux`
  * (src/attnres/_kernels/fixed_tail_sources.py:78-83), i.e.
@@ -136,7 +157,8 @@ int attnres_hip_sources_forward(const void* const* sources,
  * Source-list backward.  `sources`, `row_strides` and `grad_sources` are HOST
  * arrays of n_sources entries; grad_sources[s] is a contiguous BF16 [N, D]
  * buffer (one per list position, even when two positions hold the same
- * tensor: the caller's autograd adds them).
+ * tensor: the caller's autograd adds them).  out_refine = NULL: the
+ * recompute kernel, as for the packed backward.
  *
  * Replaces `attnres::_fixed_tail_sources_backward`
  * (fixed_tail_sources.py:85-102), i.e. `_launch_standard_backward`
@@ -161,7 +183,8 @@ int attnres_hip_sources_backward(const void* const* sources,
  * flag is nonzero, its gradient rows must already hold a BF16 gradient, and
  * the read's dv is added to it in the kernel (stored as bf16(old + dv), dv
  * in FP32); other sources' gradient rows are overwritten as in the plain
- * backward.  dq is written (not accumulated).  Several reads of the same
+ * backward.  dq is written (not accumulated).  out and out_refine are
+ * required (these entry points always use the saved refinement).  Several reads of the same
  * sources can so sum their source gradients without separate add kernels
  * (one extra read of the gradient rows instead of reading two buffers and
  * writing a third).

@@ -180,11 +180,36 @@ def test_source_fake_kernels_give_one_gradient_per_position(count):
     sources = [torch.empty(2, 3, 64, dtype=torch.bfloat16, device="meta")] * count
     query = torch.empty(16, dtype=torch.bfloat16, device="meta")
     out, refine, logit, inv_rms, stats = ops.sources_forward(sources, query, 2**-23, 1.0)
-    assert out.shape == (2, 3, 64) and refine.shape == (6, 64)
+    assert out.shape == (2, 3, 64) and refine.shape == ((6 if count > 3 else 0), 64)
     assert logit.shape == (6, count) and stats.shape == (2, 6) and stats.dtype == torch.float32
     grads = ops.sources_backward(sources, query, out, refine, out, logit, inv_rms, stats, 1.0)
     assert len(grads) == count + 1
     assert all(g.shape == (2, 3, 64) for g in grads[:count]) and grads[count].shape == (16,)
+
+
+@pytest.mark.parametrize("count", [1, 3, 4, 9])
+@pytest.mark.parametrize("layout", ["packed", "list"])
+def test_saved_state_follows_the_recompute_policy(count, layout):
+    """Reads of at most 3 sources keep neither the output nor its refinement
+    for the backward; larger reads keep both (1 + 2 bytes per element besides
+    the inputs and the per-token statistics).  Reference policy:
+    fla_full_sources.py:146-161."""
+    ops = _ops()
+    tokens, width = 6, 64
+    values = torch.empty(count, tokens, width, dtype=torch.bfloat16, device="meta", requires_grad=True)
+    query = torch.empty(16, dtype=torch.bfloat16, device="meta", requires_grad=True)
+    saved = []
+    inputs = [values, query] if layout == "packed" else [*values.unbind(0), query]
+    with torch.autograd.graph.saved_tensors_hooks(lambda t: saved.append(t) or t, lambda t: t):
+        if layout == "packed":
+            out, refine, *_ = ops.packed_forward(values, query, 2**-23, 1.0)
+        else:
+            out, refine, *_ = ops.sources_forward(inputs[:-1], query, 2**-23, 1.0)
+    saves = count > 3
+    assert refine.shape == ((tokens if saves else 0), width)
+    state = [t for t in saved if not any(t is x for x in inputs)]
+    row_state = [t for t in state if t.dim() == 2 and t.shape[-1] == width]
+    assert sum(t.numel() * t.element_size() for t in row_state) == (3 * tokens * width if saves else 0)
 
 
 def test_row_layout_flattening():

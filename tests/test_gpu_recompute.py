@@ -1,0 +1,113 @@
+"""The save/recompute policy on the GPU: reads of at most 3 sources store no
+output refinement, and their backward (`attnres_bwd_recompute_kernel`) gets
+delta = <dO, o> = sum_s p_s <v_s, dO> from the value rows.
+
+Checked against the CPU oracle on every row geometry (group of 16/32/64
+lanes, one or several chunks per lane, a whole workgroup per token above
+D = 2048), with and without key masks, on the vectorised (aligned) and the
+element-wise (padded rows) path, packed and as a source list; and against
+the saved-refinement backward on the same inputs, which computes the same
+gradients from the saved output instead (reference policy: recompute for
+S <= 3, `src/attnres/_kernels/fla_full_sources.py:146-161`).
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from attnres import _ops, attnres
+from helpers import SEEDS, compare, oracle_grads
+
+pytestmark = pytest.mark.gpu
+
+# (width, rank): geometry (lanes, chunks) -- 16x1 masked, 32x1, 64x1, 64x2 masked,
+# 64x4, 64x8 (run as 256x2) with and without masks, 256x4 with and without masks
+WIDTHS = [(128, 40), (256, 256), (512, 512), (1000, 96), (2048, 2048), (3000, 257), (4096, 4096),
+          (6144, 1024), (8192, 8192)]
+
+
+def _inputs(sources, tokens, width, rank, padded, seed):
+    torch.manual_seed(seed)
+    pad = 7 if padded else 0
+    producer = torch.randn(sources, tokens, width + pad, device="cuda", dtype=torch.bfloat16)
+    producer = producer * torch.linspace(0.5, 4, sources, device="cuda", dtype=torch.bfloat16)[:, None, None]
+    producer.requires_grad_()
+    query = (torch.randn(rank, device="cuda", dtype=torch.bfloat16) / math.sqrt(rank)).requires_grad_()
+    upstream = torch.randn(tokens, width, device="cuda", dtype=torch.bfloat16)
+    return producer, query, upstream
+
+
+@pytest.mark.parametrize("layout", ["packed", "list"])
+@pytest.mark.parametrize("padded", [False, True], ids=["aligned", "padded"])
+@pytest.mark.parametrize("width,rank", WIDTHS, ids=lambda v: str(v))
+@pytest.mark.parametrize("sources", [1, 2, 3])
+def test_recompute_backward_matches_oracle(sources, width, rank, padded, layout):
+    tokens = 37
+    producer, query, upstream = _inputs(sources, tokens, width, rank, padded, SEEDS[0] + width + sources)
+
+    def make(leaves, q):
+        values = leaves[0][..., :width]
+        return (tuple(values.unbind(0)) if layout == "list" else values), q
+
+    print(f"recompute S={sources} D={width} R={rank} padded={padded} layout={layout}", flush=True)
+    actual = attnres(make([producer], query)[0], query)
+    grads = torch.autograd.grad(actual, (producer, query), upstream)
+    expected, expected_grads = oracle_grads(make, [producer], query, upstream)
+    torch.cuda.synchronize()
+    for a, e in zip((actual, *grads), (expected, *expected_grads)):
+        compare(a, e)
+
+
+@pytest.mark.parametrize("layout", ["packed", "list"])
+@pytest.mark.parametrize("width,rank", [(1000, 96), (2048, 2048), (4096, 1024), (8192, 8192)],
+                         ids=lambda v: str(v))
+@pytest.mark.parametrize("sources", [2, 3])
+def test_recompute_agrees_with_the_saved_refinement_path(sources, width, rank, layout):
+    """Same inputs through both backward kernels: the forward output is the
+    same bits, dv agrees to BF16 rounding and dq to FP32 rounding of delta."""
+    tokens = 513
+    producer, query, upstream = _inputs(sources, tokens, width, rank, False, SEEDS[1] + width)
+    values = producer.detach()
+    q = query.detach()
+    print(f"recompute vs saved S={sources} D={width} R={rank} layout={layout}", flush=True)
+    results = {}
+    for save in (False, True):
+        if layout == "packed":
+            out, refine, logit, inv_rms, stats = _ops.packed_forward_impl(values, q, 2**-23, 1.0, save)
+            dv, dq = _ops.packed_backward(values, q, out, refine, upstream, logit, inv_rms, stats, 1.0)
+        else:
+            listed = list(values.unbind(0))
+            out, refine, logit, inv_rms, stats = _ops.sources_forward_impl(listed, q, 2**-23, 1.0, save)
+            grads = _ops.sources_backward(listed, q, out, refine, upstream, logit, inv_rms, stats, 1.0)
+            dv, dq = torch.stack(grads[:-1]), grads[-1]
+        assert refine.shape[0] == (tokens if save else 0)
+        results[save] = (out, dv, dq)
+    torch.cuda.synchronize()
+    (out_r, dv_r, dq_r), (out_s, dv_s, dq_s) = results[False], results[True]
+    assert torch.equal(out_r, out_s)
+    scale_dv = float(dv_s.float().abs().max())
+    torch.testing.assert_close(dv_r.float(), dv_s.float(), rtol=2.0**-7, atol=2.0**-9 * scale_dv)
+    rel = float((dq_r.float() - dq_s.float()).norm() / dq_s.float().norm())
+    assert rel < 2e-3, rel
+
+
+def test_recompute_special_cases_are_exact():
+    """S = 1: dv == dO, dq == 0; two identical sources: dv == dO / 2, dq == 0
+    (delta = sum_s p_s dw_s equals dw exactly when p is 1 or 1/2)."""
+    torch.manual_seed(SEEDS[2])
+    upstream = torch.randn(19, 2048, device="cuda", dtype=torch.bfloat16)
+    one = torch.randn(1, 19, 2048, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    query = torch.randn(2048, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    out = attnres(one, query)
+    dv, dq = torch.autograd.grad(out, (one, query), upstream)
+    assert torch.equal(out, one[0]) and torch.equal(dv[0], upstream)
+    assert torch.count_nonzero(dq) == 0
+    twin = one.detach().expand(2, -1, -1).contiguous().requires_grad_()
+    out = attnres(twin, query, scale=3.0)
+    dv, dq = torch.autograd.grad(out, (twin, query), upstream)
+    assert torch.equal(out, twin[0])
+    assert torch.equal(dv, (upstream.float() / 2).to(torch.bfloat16).expand(2, -1, -1))
+    assert torch.count_nonzero(dq) == 0

@@ -79,7 +79,9 @@ def test_each_backward_pass_starts_a_fresh_sum():
 
 
 def test_unused_reads_and_sources_without_grad():
-    src, queries, grads, scales = _case(sources=3, tokens=(40,), width=256, rank=64, reads=2)
+    # 4 sources: attnres saves the refinement too (smaller reads use the recompute
+    # kernel, SharedSources always the saved one), so the results are bit-identical
+    src, queries, grads, scales = _case(sources=4, tokens=(40,), width=256, rank=64, reads=2)
     src[1].requires_grad_(False)
     bank = SharedSources(src)
     used = bank.read(queries[0])
