@@ -77,6 +77,9 @@ CONFIGS = {
                    name="save/recompute policy: reads of S=1..3 at N=16384, D in {1024,2048,4096}, R=D, packed"),
     "model": dict(layers=24, width=1024, heads=16, ffn=2816, batch=16, sequence=1024, vocab=8192,
                   name="24-layer Full-schedule causal LM training step, D=1024, 16x1024 tokens, FP32 outside the reads"),
+    "model_block": dict(layers=24, width=1024, heads=16, ffn=2816, batch=16, sequence=1024, vocab=8192, block_count=8,
+                        name="24-layer Block-schedule (8 blocks) causal LM training step, D=1024, 16x1024 tokens, "
+                             "FP32 outside the reads"),
 }
 
 
@@ -413,8 +416,26 @@ def run_policy(cfg: dict, steps: int, warmup: int) -> dict:
     }
 
 
+def read_sources_per_step(config) -> list[int]:
+    """Source count of every read of one model forward (benchmarks/model.py's
+    Full or Block schedule)."""
+    from benchmarks.model import block_ends
+
+    events = 2 * config.layers
+    if config.mode == "full":
+        return list(range(2, events + 2))
+    counts, completed, partial, event = [], 1, False, 0
+    for end in block_ends(events, config.block_count):
+        while event < end:
+            if event:
+                counts.append(completed + partial)
+            partial, event = True, event + 1
+        completed, partial = completed + 1, False
+    return counts + [completed]
+
+
 def run_model(cfg: dict, steps: int, warmup: int, variant: str = "both") -> dict:
-    """model: training steps of the Full-schedule causal LM (benchmarks/model.py).
+    """model / model_block: training steps of the causal LM (benchmarks/model.py).
 
     ``variant`` "both" times the plain step (the line's value) and then the
     source-bank step; "plain" or "bank" times one of them alone (for traces).
@@ -423,8 +444,10 @@ def run_model(cfg: dict, steps: int, warmup: int, variant: str = "both") -> dict
 
     from benchmarks.model import TrainingConfig, make_model, training_step
 
+    block = "block_count" in cfg
     config = TrainingConfig(**{k: cfg[k] for k in ("layers", "width", "heads", "ffn", "batch", "sequence", "vocab")},
-                            mode="full", source_layout="packed")
+                            mode="block" if block else "full", block_count=cfg.get("block_count", 2),
+                            source_layout="packed")
     n_tokens = config.batch * config.sequence
     generator = torch.Generator(device="cuda").manual_seed(0)
     tokens = torch.randint(config.vocab, (config.batch, config.sequence), device="cuda", generator=generator)
@@ -454,20 +477,25 @@ def run_model(cfg: dict, steps: int, warmup: int, variant: str = "both") -> dict
     def rounded(x, digits):
         return None if x is None else round(x, digits)
 
-    reads = 2 * config.layers
-    read_bytes_per_step = sum(sum(read_bytes(s, n_tokens, config.width)) for s in range(2, reads + 2))
+    counts = read_sources_per_step(config)
+    reads = len(counts)
+    read_bytes_per_step = sum(sum(read_bytes(s, n_tokens, config.width)) for s in counts)
+    schedule = f"{config.mode.capitalize()}-schedule"
     return {
-        "metric": "model: 24-layer Full-schedule causal LM training step (48 AttnRes reads, S=2..49), tokens/s",
+        "metric": f"model: {config.layers}-layer {schedule} causal LM training step ({reads} AttnRes reads, "
+                  f"S={min(counts)}..{max(counts)}), tokens/s",
         "value": rate(ms), "unit": "tokens/s", "n_gpus": 1, "steps": steps,
         "warmup": warmup, "ms_per_step": rounded(ms, 3), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32 model, bf16 reads", "data": "synthetic tokens (seeded)",
         "config": {"workload": cfg["name"], "layers": config.layers, "width": config.width, "heads": config.heads,
                    "ffn": config.ffn, "batch": config.batch, "sequence": config.sequence, "vocab": config.vocab,
-                   "reads_per_step": reads, "read_sources": f"2..{reads + 1}",
+                   "mode": config.mode, "block_count": config.block_count if config.mode == "block" else None,
+                   "reads_per_step": reads, "read_sources": counts,
                    "attnres_algorithmic_bytes_per_step": read_bytes_per_step},
         "loss": rounded(loss, 4),
         # the same step with the residual stream kept in an attnres.SourceBank (one BF16
-        # cast per source, prefix reads, FP32 gradient sums in the backward kernels)
+        # cast per source, slot reads, FP32 gradient sums in the backward kernels; Block:
+        # fused partial sums)
         "source_bank": {"ms_per_step": rounded(bank_ms, 3), "tokens_per_s": rate(bank_ms),
                         "loss": rounded(bank_loss, 4)},
         "roofline": None,
@@ -507,9 +535,9 @@ def main(argv=None) -> int:
 
     _native.load()  # fail loudly if the HIP library is missing
     cfg = CONFIGS[args.config]
-    if args.config in ("c4", "c5", "model", "policy"):
+    if args.config in ("c4", "c5", "model", "model_block", "policy"):
         torch.cuda.set_device(0)
-        if args.config == "model":
+        if args.config in ("model", "model_block"):
             result = run_model(cfg, args.steps, args.warmup, args.model_variant)
         else:
             run = {"c4": run_block_schedule, "c5": run_sweep, "policy": run_policy}[args.config]

@@ -18,11 +18,16 @@ cast their sources to BF16 and their output back (reference `_read`,
 model.py:279-291).  ``backend`` is ``"kernel"`` (the HIP operator) or any
 callable with the ``attnres`` signature, e.g. the CPU oracle for parity tests.
 
-``source_bank=True`` (Full schedule, HIP backend; no reference counterpart)
-keeps the residual stream in an ``attnres.SourceBank``: each source is cast to
-BF16 once, reads are prefix views of one packed buffer, and the reads'
-backward sums every source's gradient in FP32 inside the kernels, instead of
-the per-read casts, stacks and autograd additions of the plain path.
+``source_bank=True`` (HIP backend; no reference counterpart) keeps the
+residual stream in an ``attnres.SourceBank``: each source is cast to BF16
+once, reads take slots of one packed buffer, and the reads' backward sums
+every source's gradient in FP32 inside the kernels, instead of the per-read
+casts, stacks and autograd additions of the plain path.  In the Block
+schedule, completed blocks sit in slots 0..k and each running partial in a
+slot of its own; ``push_sum`` forms the partial and its BF16 copy in one
+kernel (the caller step of reference model.py:333 fused with the next read's
+cast), and the block's last partial is written straight into the next
+completed slot.
 """
 
 from __future__ import annotations
@@ -122,8 +127,8 @@ class CausalAttnResLM(nn.Module):
 
     def __init__(self, config: TrainingConfig, backend: Backend = "kernel", *, source_bank: bool = False) -> None:
         super().__init__()
-        if source_bank and (backend != "kernel" or config.mode != "full"):
-            raise ValueError("source_bank needs the HIP backend and the Full schedule")
+        if source_bank and backend != "kernel":
+            raise ValueError("source_bank needs the HIP backend")
         self.config = config
         self.backend = backend
         self.source_bank = bool(source_bank)
@@ -185,7 +190,41 @@ class CausalAttnResLM(nn.Module):
             sources.append(self._sublayer(event, x))
         return self.read(sources, self.queries[-1])
 
+    def _forward_block_bank(self, embedded: Tensor) -> Tensor:
+        from attnres import SourceBank
+
+        events = 2 * self.config.layers
+        ends = block_ends(events, self.config.block_count)
+        # slots 0..len(ends): the embedding and the completed blocks; then one per mid-block partial
+        bank = SourceBank(len(ends) + 1 + events - len(ends))
+        bank.push(embedded, slot=0)
+        completed, scratch, event = 1, len(ends) + 1, 0
+        for end in ends:
+            partial: Tensor | None = None
+            tail: int | None = None
+            while event < end:
+                if event == 0:
+                    x = embedded
+                else:
+                    query = self.queries[event - 1].to(torch.bfloat16)
+                    x = bank.read(query, count=completed, tail=tail).to(embedded.dtype)
+                emitted = self._sublayer(event, x)
+                event += 1
+                slot = completed if event == end else scratch  # the block's last partial is its completed slot
+                if slot == scratch:
+                    scratch += 1
+                if partial is None:
+                    partial = emitted
+                    bank.push(emitted, slot=slot)
+                else:
+                    partial = bank.push_sum(partial, emitted, slot=slot)
+                tail = slot
+            completed += 1
+        return bank.read(self.queries[-1].to(torch.bfloat16), count=completed).to(embedded.dtype)
+
     def _forward_block(self, embedded: Tensor) -> Tensor:
+        if self.source_bank:
+            return self._forward_block_bank(embedded)
         events = 2 * self.config.layers
         completed = [embedded]
         partial: Tensor | None = None

@@ -42,6 +42,8 @@ from . import _native
 from ._ops import _contiguous, _dq_workspace, _source_table, _stream, packed_forward_impl, sources_forward_impl
 from ._sources import _EPS, _MAX_SOURCES, _MAX_WIDTH, check_packed, check_sources
 
+_DTYPE_F32, _DTYPE_BF16 = 0, 1  # attnres_hip.h ATTNRES_DTYPE_*
+
 
 def _pass_id() -> int:
     """The running backward pass: autograd's graph-task id (-1 outside one)."""
@@ -153,25 +155,38 @@ class _Read(torch.autograd.Function):
 
 
 class SourceBank:
-    """Sources appended one at a time and read as prefixes: the residual stream
-    of a Full-schedule model, where read i sees every source pushed before it.
+    """Sources kept in numbered slots of one packed BF16 buffer and read as
+    slot lists: the residual stream of a Full- or Block-schedule model.
+
+    Full schedule (read i sees every source pushed before it)::
 
         bank = SourceBank(capacity=2 * layers + 1)
-        bank.push(embedding)                      # any float dtype, shape [..., D]
-        x = bank.read(query_0)                    # attnres over the 1 source so far (BF16 out)
-        bank.push(sublayer(x.to(dtype)))
-        x = bank.read(query_1)                    # over 2 sources, ...
+        bank.push(embedding)                      # slot 0; any float dtype, shape [..., D]
+        x = bank.read(query_0)                    # attnres over slot 0 (BF16 out)
+        bank.push(sublayer(x.to(dtype)))          # slot 1
+        x = bank.read(query_1)                    # over slots 0..1, ...
 
-    Each source is converted to BF16 once, into slot i of one packed
-    ``[capacity, ..., D]`` BF16 buffer, so a read is the prefix view
-    ``buffer[:count]`` (no per-read conversion or stack).  In the backward every
-    read adds its FP32 dv for its prefix into one FP32 ``[capacity, ..., D]``
-    buffer in the kernel (``attnres_hip_packed_backward_accumulate_f32``: the
-    first contribution to a slot writes it); slot i's sum is handed to source i
-    (in its dtype) once every read that saw it has run its backward -- source
-    i's autograd node produced the token those reads take as inputs.  The sums
-    are FP32 without BF16 rounding of the per-read dv.  Eager mode only; one
-    bank per forward pass.
+    Block schedule (a read sees the completed blocks, slots 0..k-1, plus the
+    running partial sum of the current block in some other slot)::
+
+        bank.push(embedding, slot=0)
+        bank.push(first_emitted, slot=p)          # the partial starts as one output
+        x = bank.read(query, count=1, tail=p)     # attnres(embedding, partial)
+        partial = bank.push_sum(partial, emitted, slot=q)   # partial + emitted, one pass
+
+    Each source is converted to BF16 once, into its slot, so a read passes
+    slot rows (the prefix view ``buffer[:count]``, or a list of slot pointers
+    when a tail slot is added) with no per-read conversion or stack.
+    ``push_sum`` adds the block's partial and the new output and writes the
+    sum (in their dtype, returned) and its BF16 copy (into the slot) in one
+    kernel (``attnres_hip_partial_sum``).  In the backward every read adds its
+    FP32 dv into one FP32 ``[capacity, ..., D]`` buffer in the kernel
+    (``attnres_hip_{packed,sources}_backward_accumulate_f32``: the first
+    contribution to a slot writes it); slot i's sum is handed to its source
+    (in the source's dtype) once every read that saw slot i has run its
+    backward -- the slot's push node produced the token those reads take as
+    inputs.  The sums are FP32 without BF16 rounding of the per-read dv.
+    Eager mode only; one bank per forward pass.
     """
 
     def __init__(self, capacity: int) -> None:
@@ -179,77 +194,136 @@ class SourceBank:
             raise ValueError(f"capacity must be an integer in 1..{_MAX_SOURCES}")
         self.capacity = capacity
         self._values: Tensor | None = None
-        self._tokens: list[Tensor] = []
+        self._tokens: list[Tensor | None] = [None] * capacity
         self._grads: Tensor | None = None
-        self._written: list[bool] = []
+        self._written: list[bool] = [False] * capacity
         self._pass = -1
 
     def __len__(self) -> int:
-        return len(self._tokens)
+        """Number of pushed slots."""
+        return sum(token is not None for token in self._tokens)
 
-    def push(self, source: Tensor) -> None:
-        """Append ``source`` (``[..., D]``, any float dtype, on the GPU) as the next slot."""
+    def _claim(self, source: Tensor, slot: int | None) -> int:
         if not isinstance(source, Tensor) or not source.is_floating_point():
             raise TypeError("a source must be a floating-point tensor")
         if not source.is_cuda:
             raise RuntimeError("attnres requires CUDA (ROCm/HIP) device tensors")
-        if len(self._tokens) == self.capacity:
-            raise ValueError("the source bank is full")
+        if slot is None:
+            free = [i for i, token in enumerate(self._tokens) if token is None]
+            if not free:
+                raise ValueError("the source bank is full")
+            slot = free[0]
+        if isinstance(slot, bool) or not isinstance(slot, int) or not 0 <= slot < self.capacity:
+            raise ValueError(f"slot must be an integer in 0..{self.capacity - 1}")
+        if self._tokens[slot] is not None:
+            raise ValueError(f"slot {slot} already holds a source")
         if self._values is None:
             if source.ndim < 1 or source.numel() == 0 or not 1 <= source.shape[-1] <= _MAX_WIDTH:
                 raise ValueError("each source must have shape [...,D]")
             self._values = torch.empty((self.capacity, *source.shape), device=source.device, dtype=torch.bfloat16)
         elif source.shape != self._values.shape[1:] or source.device != self._values.device:
             raise ValueError("all source tensors must have the same logical shape and device")
-        self._written.append(False)
-        self._tokens.append(_Push.apply(self, len(self._tokens), source))
+        return slot
 
-    def read(self, query: Tensor, *, count: int | None = None, eps: float = _EPS, scale: float = 1.0) -> Tensor:
-        """``attnres(first `count` sources, query)`` (all pushed so far by default), BF16."""
-        count = len(self._tokens) if count is None else count
-        if isinstance(count, bool) or not isinstance(count, int) or not 1 <= count <= len(self._tokens):
-            raise ValueError("count must select 1..len(bank) pushed sources")
-        values = self._values[:count]
-        eps_value, scale_value = check_packed(values, query, eps, scale)
-        return _BankRead.apply(self, count, query, eps_value, scale_value, *self._tokens[:count])
+    def push(self, source: Tensor, *, slot: int | None = None) -> int:
+        """Store ``source`` (``[..., D]``, any float dtype, on the GPU) in
+        ``slot`` (default: the lowest free one); returns the slot."""
+        slot = self._claim(source, slot)
+        self._tokens[slot] = _Push.apply(self, slot, source)
+        return slot
 
-    def _backward(self, count: int, query: Tensor, out: Tensor, out_refine: Tensor, grad_out: Tensor,
+    def push_sum(self, prev: Tensor, emitted: Tensor, *, slot: int | None = None) -> Tensor:
+        """``prev + emitted`` (FP32 or BF16, same shape and dtype), returned in
+        that dtype and stored as BF16 in ``slot`` -- one kernel for the
+        Block schedule's partial sum and its BF16 copy."""
+        if not isinstance(prev, Tensor) or not isinstance(emitted, Tensor):
+            raise TypeError("push_sum takes two tensors")
+        if prev.shape != emitted.shape or prev.dtype != emitted.dtype or prev.device != emitted.device:
+            raise ValueError("push_sum needs tensors of one shape, dtype and device")
+        if prev.dtype not in (torch.float32, torch.bfloat16):
+            raise TypeError("push_sum supports float32 and bfloat16 tensors")
+        slot = self._claim(emitted, slot)
+        partial, token = _PushSum.apply(self, slot, prev, emitted)
+        self._tokens[slot] = token
+        return partial
+
+    def read(self, query: Tensor, *, count: int | None = None, tail: int | None = None, eps: float = _EPS,
+             scale: float = 1.0) -> Tensor:
+        """``attnres`` over slots ``0..count-1`` (default: every pushed slot,
+        which must then be ``0..len-1``) followed by slot ``tail`` if given; BF16."""
+        if count is None:
+            if tail is not None:
+                raise ValueError("a read with a tail slot needs count")
+            count = len(self)
+        if isinstance(count, bool) or not isinstance(count, int) or not 0 <= count <= self.capacity:
+            raise ValueError("count must be a number of leading slots")
+        if any(self._tokens[i] is None for i in range(count)):
+            raise ValueError("count must select pushed slots 0..count-1")
+        slots = list(range(count))
+        if tail is not None:
+            if isinstance(tail, bool) or not isinstance(tail, int) or not count <= tail < self.capacity \
+                    or self._tokens[tail] is None:
+                raise ValueError("tail must be a pushed slot after the leading ones")
+            slots.append(tail)
+        if not slots:
+            raise ValueError("a read needs at least one source")
+        if tail is None:
+            eps_value, scale_value = check_packed(self._values[:count], query, eps, scale)
+        else:
+            _, eps_value, scale_value = check_sources(tuple(self._values[i] for i in slots), query, eps, scale)
+        return _BankRead.apply(self, tuple(slots), query, eps_value, scale_value, *[self._tokens[i] for i in slots])
+
+    def _sources(self, slots: tuple[int, ...]) -> list[Tensor]:
+        return [self._values[i] for i in slots]
+
+    def _prefix(self, slots: tuple[int, ...]) -> bool:
+        return slots == tuple(range(len(slots)))
+
+    def _backward(self, slots: tuple[int, ...], query: Tensor, out: Tensor, out_refine: Tensor, grad_out: Tensor,
                   logit: Tensor, inv_rms: Tensor, stats: Tensor, scale: float) -> Tensor:
         lib = _native.load()
-        values = self._values[:count]
-        width = int(values.shape[-1])
-        tokens = values[0].numel() // width
+        count = len(slots)
+        width = int(self._values.shape[-1])
+        tokens = self._values[0].numel() // width
         rank = query.numel()
-        device = values.device
+        device = self._values.device
         current = _pass_id()
         if self._pass != current:
             # first read of this pass: a fresh buffer, so sums handed out by an earlier pass
             # (views of its buffer) stay valid and a pass that stopped short leaves nothing behind
             self._grads = torch.empty(self._values.shape, device=device, dtype=torch.float32)
-            self._written = [False] * len(self._written)
+            self._written = [False] * self.capacity
             self._pass = current
-        flags = (ctypes.c_uint8 * count)(*[1 if written else 0 for written in self._written[:count]])
+        flags = (ctypes.c_uint8 * count)(*[1 if self._written[i] else 0 for i in slots])
         grad_query = torch.empty((rank,), device=device, dtype=torch.bfloat16)
         workspace = _dq_workspace(lib, tokens, width, rank, device)
         grad_out = _contiguous(grad_out.to(torch.bfloat16))
+        saved = (_contiguous(out).data_ptr(), _contiguous(out_refine).data_ptr(), grad_out.data_ptr(),
+                 _contiguous(logit).data_ptr(), _contiguous(inv_rms).data_ptr(), _contiguous(stats).data_ptr())
         with torch.cuda.device(device):
-            status = lib.attnres_hip_packed_backward_accumulate_f32(
-                values.data_ptr(), tokens * width, width, count, tokens, width, query.data_ptr(), rank, scale,
-                _contiguous(out).data_ptr(), _contiguous(out_refine).data_ptr(), grad_out.data_ptr(),
-                _contiguous(logit).data_ptr(), _contiguous(inv_rms).data_ptr(), _contiguous(stats).data_ptr(),
-                self._grads.data_ptr(), grad_query.data_ptr(), workspace.data_ptr(), workspace.numel(), flags,
-                _stream(device))
+            if self._prefix(slots):
+                status = lib.attnres_hip_packed_backward_accumulate_f32(
+                    self._values.data_ptr(), tokens * width, width, count, tokens, width, query.data_ptr(), rank,
+                    scale, *saved, self._grads.data_ptr(), grad_query.data_ptr(), workspace.data_ptr(),
+                    workspace.numel(), flags, _stream(device))
+            else:
+                pointers = (ctypes.c_void_p * count)(*[self._values[i].data_ptr() for i in slots])
+                strides = (ctypes.c_int64 * count)(*([width] * count))
+                sums = (ctypes.c_void_p * count)(*[self._grads[i].data_ptr() for i in slots])
+                status = lib.attnres_hip_sources_backward_accumulate_f32(
+                    pointers, strides, count, tokens, width, query.data_ptr(), rank, scale, *saved, sums,
+                    grad_query.data_ptr(), workspace.data_ptr(), workspace.numel(), flags, _stream(device))
         _native.check(status, "attnres source-bank backward")
-        for slot in range(count):
-            self._written[slot] = True
+        for i in slots:
+            self._written[i] = True
         return grad_query
 
-    def _take(self, slot: int, dtype: torch.dtype) -> Tensor | None:
-        """Slot `slot`'s FP32 sum in `dtype` (a view of this pass's buffer when FP32)."""
+    def _take(self, slot: int) -> Tensor | None:
+        """Slot `slot`'s FP32 sum (a view of this pass's buffer), or None."""
         if self._pass != _pass_id() or not self._written[slot]:
             return None
         self._written[slot] = False
-        return self._grads[slot].to(dtype)
+        return self._grads[slot]
 
 
 class _Push(torch.autograd.Function):
@@ -261,30 +335,65 @@ class _Push(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, _token_grad):
-        return None, None, ctx.bank._take(ctx.slot, ctx.dtype)
+        grad = ctx.bank._take(ctx.slot)
+        return None, None, None if grad is None else grad.to(ctx.dtype)
+
+
+class _PushSum(torch.autograd.Function):
+    """partial = prev + emitted, with its BF16 copy written into the slot by
+    the same kernel; the gradient of both inputs is that of the partial plus
+    the slot's summed read gradient."""
+
+    @staticmethod
+    def forward(ctx, bank: SourceBank, slot: int, prev: Tensor, emitted: Tensor):
+        lib = _native.load()
+        prev, emitted = _contiguous(prev.detach()), _contiguous(emitted.detach())
+        partial = torch.empty_like(emitted)
+        dtype = _DTYPE_F32 if emitted.dtype == torch.float32 else _DTYPE_BF16
+        with torch.cuda.device(emitted.device):
+            status = lib.attnres_hip_partial_sum(prev.data_ptr(), emitted.data_ptr(), dtype, emitted.numel(),
+                                                 partial.data_ptr(), bank._values[slot].data_ptr(),
+                                                 _stream(emitted.device))
+        _native.check(status, "attnres partial sum")
+        ctx.bank, ctx.slot, ctx.dtype = bank, slot, emitted.dtype
+        return partial, emitted.new_empty((0,))
+
+    @staticmethod
+    def backward(ctx, grad_partial, _token_grad):
+        grad = ctx.bank._take(ctx.slot)
+        if grad is not None:
+            grad = grad.to(ctx.dtype) if grad_partial is None else grad_partial + grad.to(ctx.dtype)
+        else:
+            grad = grad_partial
+        return None, None, grad, grad
 
 
 class _BankRead(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, bank: SourceBank, count: int, query: Tensor, eps: float, scale: float,
+    def forward(ctx, bank: SourceBank, slots: tuple[int, ...], query: Tensor, eps: float, scale: float,
                 *tokens: Tensor) -> Tensor:
         query = _contiguous(query)
-        values = bank._values[:count]
-        flat = values.reshape(count, -1, values.shape[-1])  # a view: the bank is contiguous
-        out, out_refine, logit, inv_rms, stats = packed_forward_impl(flat, query, eps, scale, True)
-        ctx.bank, ctx.count, ctx.scale = bank, count, scale
+        shape = bank._values.shape[1:]
+        if bank._prefix(slots):
+            flat = bank._values[:len(slots)].reshape(len(slots), -1, shape[-1])  # a view: the bank is contiguous
+            out, out_refine, logit, inv_rms, stats = packed_forward_impl(flat, query, eps, scale, True)
+        else:
+            out, out_refine, logit, inv_rms, stats = sources_forward_impl(bank._sources(slots), query, eps, scale,
+                                                                         True)
+        # always saved: the accumulating kernels read the refinement
+        ctx.bank, ctx.slots, ctx.scale = bank, slots, scale
         ctx.token_device = tokens[0].device
         ctx.save_for_backward(query, out, out_refine, logit, inv_rms, stats)
-        return out.reshape(values.shape[1:])
+        return out.reshape(shape)
 
     @staticmethod
     def backward(ctx, grad_out):
         query, out, out_refine, logit, inv_rms, stats = ctx.saved_tensors
-        grad_query = ctx.bank._backward(ctx.count, query, out, out_refine, grad_out, logit, inv_rms, stats,
+        grad_query = ctx.bank._backward(ctx.slots, query, out, out_refine, grad_out, logit, inv_rms, stats,
                                         ctx.scale)
         empty = torch.empty((0,), device=ctx.token_device)
         return (None, None, grad_query if ctx.needs_input_grad[2] else None, None, None,
-                *([empty] * ctx.count))
+                *([empty] * len(ctx.slots)))
 
 
 __all__ = ["SharedSources", "SourceBank"]

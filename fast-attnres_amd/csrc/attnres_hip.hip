@@ -13,6 +13,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdint>
@@ -30,6 +31,8 @@ ATTNRES_FOR_EACH_GEOMETRY(ATTNRES_DECLARE_GEOMETRY_RECOMPUTE)
 namespace {
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 // FP32 to BF16, round-to-nearest-even (v_cvt_pk_bf16_f32).
@@ -37,6 +40,12 @@ __device__ __forceinline__ uint16_t to_bf16(float x) {
   f32x2 v = {x, 0.0f};
   bf16x2 b = __builtin_convertvector(v, bf16x2);
   return static_cast<uint16_t>(__builtin_bit_cast(uint32_t, b) & 0xffffu);
+}
+
+// Two FP32 values to packed BF16 (low element first), round-to-nearest-even.
+__device__ __forceinline__ uint32_t pack2_bf16(float lo, float hi) {
+  f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
 // The dq reduction is latency-bound (a few MB): each thread issues all of its
@@ -81,6 +90,108 @@ __global__ void __launch_bounds__(kBlock) attnres_dq_finalize_kernel(
   for (int p = 0; p < kFinalizeSlices; ++p) t = p < P ? t + v[p] : t;
   dq32[col] = t;
   dq16[col] = to_bf16(t);
+}
+
+// Block-schedule partial sum: out = prev + emitted in FP32 arithmetic, stored
+// in the inputs' dtype (T), and bf16(out) for the read that takes the partial
+// as a source -- the add and the BF16 staging in one pass.  Thread i handles
+// elements [8i, 8i + 8): 16/32-byte loads and stores when VEC (pointers 16-byte
+// aligned and n % 8 == 0), else element by element.
+template <typename T>
+__device__ __forceinline__ float load_as_f32(const T* p, int64_t i) {
+  if constexpr (std::is_same_v<T, float>) {
+    return p[i];
+  } else {
+    return __uint_as_float(static_cast<uint32_t>(p[i]) << 16);
+  }
+}
+
+template <typename T, bool VEC>
+__global__ void __launch_bounds__(kBlock) attnres_partial_sum_kernel(const T* __restrict__ prev,
+                                                                     const T* __restrict__ emitted, int64_t n,
+                                                                     T* __restrict__ out,
+                                                                     uint16_t* __restrict__ out_bf16) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock * kVec;
+  for (int64_t i0 = (static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x) * kVec; i0 < n; i0 += stride) {
+    float x[kVec];
+    if constexpr (VEC) {
+      if constexpr (std::is_same_v<T, float>) {
+        const f32x4* a = reinterpret_cast<const f32x4*>(prev + i0);
+        const f32x4* b = reinterpret_cast<const f32x4*>(emitted + i0);
+        const f32x4 a0 = __builtin_nontemporal_load(a), a1 = __builtin_nontemporal_load(a + 1);
+        const f32x4 b0 = __builtin_nontemporal_load(b), b1 = __builtin_nontemporal_load(b + 1);
+        const f32x4 s0 = a0 + b0, s1 = a1 + b1;
+        __builtin_nontemporal_store(s0, reinterpret_cast<f32x4*>(out + i0));
+        __builtin_nontemporal_store(s1, reinterpret_cast<f32x4*>(out + i0) + 1);
+        x[0] = s0.x; x[1] = s0.y; x[2] = s0.z; x[3] = s0.w;
+        x[4] = s1.x; x[5] = s1.y; x[6] = s1.z; x[7] = s1.w;
+      } else {
+        const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(prev + i0));
+        const u32x4 b = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(emitted + i0));
+        const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          x[2 * j] = __uint_as_float(aw[j] << 16) + __uint_as_float(bw[j] << 16);
+          x[2 * j + 1] = __uint_as_float(aw[j] & 0xffff0000u) + __uint_as_float(bw[j] & 0xffff0000u);
+        }
+      }
+      u32x4 w;
+      w.x = pack2_bf16(x[0], x[1]);
+      w.y = pack2_bf16(x[2], x[3]);
+      w.z = pack2_bf16(x[4], x[5]);
+      w.w = pack2_bf16(x[6], x[7]);
+      __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(out_bf16 + i0));
+      if constexpr (!std::is_same_v<T, float>) __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(out + i0));
+    } else {
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) {
+        const int64_t i = i0 + e;
+        if (i < n) {
+          const float v = load_as_f32(prev, i) + load_as_f32(emitted, i);
+          const uint16_t h = to_bf16(v);
+          out_bf16[i] = h;
+          if constexpr (std::is_same_v<T, float>) {
+            out[i] = v;
+          } else {
+            out[i] = h;
+          }
+        }
+      }
+    }
+  }
+}
+
+int launch_status(const char* what);
+
+int launch_partial_sum(const void* prev, const void* emitted, bool f32, int64_t n, void* out, void* out_bf16,
+                       hipStream_t stream) {
+  const bool vec = n % kVec == 0 && ((reinterpret_cast<uintptr_t>(prev) | reinterpret_cast<uintptr_t>(emitted) |
+                                      reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(out_bf16)) &
+                                     15u) == 0;
+  const int64_t threads = (n + kVec - 1) / kVec;
+  const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((threads + kBlock - 1) / kBlock, 65536));
+  if (f32) {
+    if (vec) {
+      hipLaunchKernelGGL((attnres_partial_sum_kernel<float, true>), dim3(blocks), dim3(kBlock), 0, stream,
+                         static_cast<const float*>(prev), static_cast<const float*>(emitted), n,
+                         static_cast<float*>(out), static_cast<uint16_t*>(out_bf16));
+    } else {
+      hipLaunchKernelGGL((attnres_partial_sum_kernel<float, false>), dim3(blocks), dim3(kBlock), 0, stream,
+                         static_cast<const float*>(prev), static_cast<const float*>(emitted), n,
+                         static_cast<float*>(out), static_cast<uint16_t*>(out_bf16));
+    }
+  } else {
+    if (vec) {
+      hipLaunchKernelGGL((attnres_partial_sum_kernel<uint16_t, true>), dim3(blocks), dim3(kBlock), 0, stream,
+                         static_cast<const uint16_t*>(prev), static_cast<const uint16_t*>(emitted), n,
+                         static_cast<uint16_t*>(out), static_cast<uint16_t*>(out_bf16));
+    } else {
+      hipLaunchKernelGGL((attnres_partial_sum_kernel<uint16_t, false>), dim3(blocks), dim3(kBlock), 0, stream,
+                         static_cast<const uint16_t*>(prev), static_cast<const uint16_t*>(emitted), n,
+                         static_cast<uint16_t*>(out), static_cast<uint16_t*>(out_bf16));
+    }
+  }
+  return launch_status("attnres partial sum");
 }
 
 // ---------------------------------------------------------------- host side
@@ -133,7 +244,7 @@ int launch_forward(const FwdArgs<Rows>& a, bool vec, hipStream_t stream) {
 // always the accumulating kernel (its first write leaves every bit clear).
 template <int G, int CH, class Rows, class Grads>
 int64_t launch_bwd_geometry_any(const BwdArgs<Rows, Grads>& a, bool nomask, bool vec, bool acc, hipStream_t stream) {
-  if constexpr (std::is_same_v<Grads, PackedGradsF32>) {
+  if constexpr (kF32Grads<Grads>) {
     (void)acc;
     return launch_bwd_geometry_f32<G, CH>(a, nomask, vec, stream);
   } else {
@@ -145,7 +256,7 @@ int64_t launch_bwd_geometry_any(const BwdArgs<Rows, Grads>& a, bool nomask, bool
 template <int G, int CH, class Rows, class Grads>
 int64_t launch_bwd_select(const BwdArgs<Rows, Grads>& a, bool nomask, bool vec, bool acc, bool recompute,
                           hipStream_t stream) {
-  if constexpr (!std::is_same_v<Grads, PackedGradsF32>) {
+  if constexpr (!kF32Grads<Grads>) {
     if (recompute) return launch_bwd_recompute_geometry<G, CH>(a, nomask, vec, stream);
   }
   return launch_bwd_geometry_any<G, CH>(a, nomask, vec, acc, stream);
@@ -279,7 +390,7 @@ int packed_backward(const void* values, int64_t source_stride, int64_t row_strid
                     const float* inv_rms, const float* stats, void* grad_values, void* grad_query,
                     float* dq_workspace, int64_t dq_workspace_elems, const uint8_t* accumulate, bool need_flags,
                     void* stream) {
-  constexpr bool kF32 = std::is_same_v<Grads, PackedGradsF32>;
+  constexpr bool kF32 = kF32Grads<Grads>;
   const char* name = kF32 ? "attnres_hip_packed_backward_accumulate_f32"
                      : need_flags ? "attnres_hip_packed_backward_accumulate" : "attnres_hip_packed_backward";
   int st = check_shape(n_sources, n_tokens, width, rank);
@@ -408,13 +519,16 @@ int attnres_hip_sources_forward(const void* const* sources, const int64_t* row_s
 namespace attnres_hip {
 namespace {
 
+template <class Grads = ListGrads>
 int sources_backward(const void* const* sources, const int64_t* row_strides, int64_t n_sources,
                      int64_t n_tokens, int64_t width, const void* query, int64_t rank, float scale,
                      const void* out, const int8_t* out_refine, const void* grad_out, const float* logit,
                      const float* inv_rms, const float* stats, void* const* grad_sources, void* grad_query,
                      float* dq_workspace, int64_t dq_workspace_elems, const uint8_t* accumulate, bool need_flags,
                      void* stream) {
-  const char* name = need_flags ? "attnres_hip_sources_backward_accumulate" : "attnres_hip_sources_backward";
+  constexpr bool kF32 = kF32Grads<Grads>;
+  const char* name = kF32 ? "attnres_hip_sources_backward_accumulate_f32"
+                     : need_flags ? "attnres_hip_sources_backward_accumulate" : "attnres_hip_sources_backward";
   int st = check_shape(n_sources, n_tokens, width, rank);
   if (st) return st;
   const bool recompute = !need_flags && !out_refine;
@@ -427,7 +541,7 @@ int sources_backward(const void* const* sources, const int64_t* row_strides, int
   if (dq_workspace_elems < need)
     return fail(ATTNRES_ERR_WORKSPACE, "dq workspace has %lld elements, needs %lld",
                 (long long)dq_workspace_elems, (long long)need);
-  BwdArgs<ListRows, ListGrads> a{};
+  BwdArgs<ListRows, Grads> a{};
   bool vec = width % kVec == 0 && aligned16_or_null(out) && aligned16_or_null(out_refine) && aligned16(grad_out);
   for (int64_t s = 0; s < n_sources; ++s) {
     if (!sources[s] || !grad_sources[s])
@@ -435,7 +549,7 @@ int sources_backward(const void* const* sources, const int64_t* row_strides, int
     if (row_strides[s] < 0) return fail(ATTNRES_ERR_STRIDE, "source %lld has a negative row stride", (long long)s);
     a.src.ptr[s] = static_cast<const uint16_t*>(sources[s]);
     a.src.row_stride[s] = row_strides[s];
-    a.grad.ptr[s] = static_cast<uint16_t*>(grad_sources[s]);
+    a.grad.ptr[s] = static_cast<std::remove_reference_t<decltype(a.grad.ptr[0])>>(grad_sources[s]);
     vec = vec && aligned16(sources[s]) && aligned16(grad_sources[s]) &&
           (row_strides[s] % kVec == 0 || n_tokens == 1);
   }
@@ -488,6 +602,31 @@ int attnres_hip_sources_backward_accumulate(const void* const* sources, const in
   return sources_backward(sources, row_strides, n_sources, n_tokens, width, query, rank, scale, out, out_refine,
                           grad_out, logit, inv_rms, stats, grad_sources, grad_query, dq_workspace,
                           dq_workspace_elems, accumulate, true, stream);
+}
+
+int attnres_hip_sources_backward_accumulate_f32(const void* const* sources, const int64_t* row_strides,
+                                                int64_t n_sources, int64_t n_tokens, int64_t width,
+                                                const void* query, int64_t rank, float scale, const void* out,
+                                                const int8_t* out_refine, const void* grad_out,
+                                                const float* logit, const float* inv_rms, const float* stats,
+                                                float* const* grad_sums, void* grad_query, float* dq_workspace,
+                                                int64_t dq_workspace_elems, const uint8_t* accumulate,
+                                                void* stream) {
+  return sources_backward<ListGradsF32>(sources, row_strides, n_sources, n_tokens, width, query, rank, scale, out,
+                                        out_refine, grad_out, logit, inv_rms, stats,
+                                        reinterpret_cast<void* const*>(grad_sums), grad_query, dq_workspace,
+                                        dq_workspace_elems, accumulate, true, stream);
+}
+
+int attnres_hip_partial_sum(const void* prev, const void* emitted, int dtype, int64_t n_elems, void* out,
+                            void* out_bf16, void* stream) {
+  if (!prev || !emitted || !out || !out_bf16)
+    return fail(ATTNRES_ERR_NULL_POINTER, "null pointer argument to attnres_hip_partial_sum");
+  if (dtype != ATTNRES_DTYPE_F32 && dtype != ATTNRES_DTYPE_BF16)
+    return fail(ATTNRES_ERR_SHAPE, "dtype=%d is neither ATTNRES_DTYPE_F32 nor ATTNRES_DTYPE_BF16", dtype);
+  if (n_elems < 1) return fail(ATTNRES_ERR_SHAPE, "n_elems=%lld must be positive", (long long)n_elems);
+  return launch_partial_sum(prev, emitted, dtype == ATTNRES_DTYPE_F32, n_elems, out, out_bf16,
+                            static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

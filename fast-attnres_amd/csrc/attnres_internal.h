@@ -74,6 +74,23 @@ struct PackedGradsF32 {
   }
 };
 
+// FP32 gradient sums of a source list: one contiguous [N, D] FP32 buffer per
+// position (the slots of a source bank read as a list).
+struct ListGradsF32 {
+  float* ptr[kMaxSources];
+  __device__ __forceinline__ float* row(int s, int64_t n, int d) const {
+    return ptr[s] + n * d;
+  }
+};
+
+// Gradient types whose rows are FP32 sums (written or added without rounding).
+template <class Grads>
+inline constexpr bool kF32Grads = false;
+template <>
+inline constexpr bool kF32Grads<PackedGradsF32> = true;
+template <>
+inline constexpr bool kF32Grads<ListGradsF32> = true;
+
 template <class Rows>
 struct FwdArgs {
   Rows src;
@@ -181,14 +198,15 @@ int64_t launch_bwd_recompute_geometry(const BwdArgs<Rows, Grads>& a, bool nomask
   extern template int64_t launch_bwd_recompute_geometry<G, CH, ListRows, ListGrads>(            \
       const BwdArgs<ListRows, ListGrads>&, bool, bool, hipStream_t);
 
-// The accumulating backward into FP32 gradient sums (packed sources only).
-template <int G, int CH>
-int64_t launch_bwd_geometry_f32(const BwdArgs<PackedRows, PackedGradsF32>& a, bool nomask, bool vec,
-                                hipStream_t stream);
+// The accumulating backward into FP32 gradient sums.
+template <int G, int CH, class Rows, class Grads>
+int64_t launch_bwd_geometry_f32(const BwdArgs<Rows, Grads>& a, bool nomask, bool vec, hipStream_t stream);
 
-#define ATTNRES_DECLARE_GEOMETRY_F32(G, CH)                                                          \
-  extern template int64_t launch_bwd_geometry_f32<G, CH>(const BwdArgs<PackedRows, PackedGradsF32>&, \
-                                                         bool, bool, hipStream_t);
+#define ATTNRES_DECLARE_GEOMETRY_F32(G, CH)                                                       \
+  extern template int64_t launch_bwd_geometry_f32<G, CH, PackedRows, PackedGradsF32>(             \
+      const BwdArgs<PackedRows, PackedGradsF32>&, bool, bool, hipStream_t);                       \
+  extern template int64_t launch_bwd_geometry_f32<G, CH, ListRows, ListGradsF32>(                 \
+      const BwdArgs<ListRows, ListGradsF32>&, bool, bool, hipStream_t);
 
 #define ATTNRES_FOR_EACH_GEOMETRY(X) X(16, 1) X(32, 1) X(64, 1) X(64, 2) X(64, 4) X(64, 8) X(256, 4)
 

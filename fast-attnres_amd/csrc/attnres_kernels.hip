@@ -666,11 +666,11 @@ struct GradRows {
 // a.accumulate, the item's gradient row is prefetched with its value row (a
 // second ring; other items load the idle row, so every load stays
 // unconditional) and dv is stored as bf16(old + dv).
-// With PackedGradsF32 gradients (a source bank's FP32 sums) the rows are FP32:
-// dv is written, or added, without BF16 rounding.
+// With FP32 gradients (PackedGradsF32 / ListGradsF32: a source bank's sums)
+// the rows are FP32: dv is written, or added, without BF16 rounding.
 template <int G, int CH, int NB, bool NOMASK, bool VEC, bool ACC, class Rows, class Grads>
 __global__ void __launch_bounds__(kBlock) attnres_bwd_kernel(const BwdArgs<Rows, Grads> a) {
-  constexpr bool kF32 = std::is_same_v<Grads, PackedGradsF32>;
+  constexpr bool kF32 = kF32Grads<Grads>;
   static_assert(!kF32 || ACC, "FP32 gradient sums use the accumulating variant");
   static_assert(G <= 64 || G == kBlock, "a wide group is the whole workgroup");
   constexpr int kGroups = kBlock / G;
@@ -1109,9 +1109,8 @@ int64_t launch_bwd_recompute_geometry(const BwdArgs<Rows, Grads>& a, bool nomask
              : launch_bwd_recompute<RG, RCH, false, false>(a, stream);
 }
 
-template <int G, int CH>
-int64_t launch_bwd_geometry_f32(const BwdArgs<PackedRows, PackedGradsF32>& a, bool nomask, bool vec,
-                                hipStream_t stream) {
+template <int G, int CH, class Rows, class Grads>
+int64_t launch_bwd_geometry_f32(const BwdArgs<Rows, Grads>& a, bool nomask, bool vec, hipStream_t stream) {
   return launch_bwd_variant<G, CH, true>(a, nomask, vec, stream);
 }
 
@@ -1124,8 +1123,10 @@ template int64_t launch_bwd_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, PackedRows, 
     const BwdArgs<PackedRows, PackedGrads>&, bool, bool, bool, hipStream_t);
 template int64_t launch_bwd_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, ListRows, ListGrads>(
     const BwdArgs<ListRows, ListGrads>&, bool, bool, bool, hipStream_t);
-template int64_t launch_bwd_geometry_f32<ATTNRES_LANES, ATTNRES_CHUNKS>(const BwdArgs<PackedRows, PackedGradsF32>&,
-                                                                        bool, bool, hipStream_t);
+template int64_t launch_bwd_geometry_f32<ATTNRES_LANES, ATTNRES_CHUNKS, PackedRows, PackedGradsF32>(
+    const BwdArgs<PackedRows, PackedGradsF32>&, bool, bool, hipStream_t);
+template int64_t launch_bwd_geometry_f32<ATTNRES_LANES, ATTNRES_CHUNKS, ListRows, ListGradsF32>(
+    const BwdArgs<ListRows, ListGradsF32>&, bool, bool, hipStream_t);
 template int64_t launch_bwd_recompute_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, PackedRows, PackedGrads>(
     const BwdArgs<PackedRows, PackedGrads>&, bool, bool, hipStream_t);
 template int64_t launch_bwd_recompute_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, ListRows, ListGrads>(

@@ -69,6 +69,10 @@ enum attnres_status {
 /* Reads of at most this many sources may skip the refinement (see above). */
 #define ATTNRES_RECOMPUTE_MAX_SOURCES 3
 
+/* Element types of attnres_hip_partial_sum. */
+#define ATTNRES_DTYPE_F32 0
+#define ATTNRES_DTYPE_BF16 1
+
 /* Library version string, e.g. "1.0.0". */
 const char* attnres_hip_version(void);
 
@@ -233,6 +237,38 @@ int attnres_hip_sources_backward_accumulate(const void* const* sources,
                                             void* grad_query, float* dq_workspace,
                                             int64_t dq_workspace_elems,
                                             const uint8_t* accumulate, void* stream);
+
+/*
+ * Source-list form of attnres_hip_packed_backward_accumulate_f32:
+ * `grad_sums` is a HOST array of n_sources pointers to contiguous FP32 [N, D]
+ * buffers (for a source bank whose reads take some slots as a list: the
+ * Block schedule's completed blocks plus the running partial).  No
+ * counterpart in the reference; used by attnres.SourceBank.
+ */
+int attnres_hip_sources_backward_accumulate_f32(const void* const* sources,
+                                                const int64_t* row_strides, int64_t n_sources,
+                                                int64_t n_tokens, int64_t width,
+                                                const void* query, int64_t rank, float scale,
+                                                const void* out, const int8_t* out_refine,
+                                                const void* grad_out, const float* logit,
+                                                const float* inv_rms, const float* stats,
+                                                float* const* grad_sums,
+                                                void* grad_query, float* dq_workspace,
+                                                int64_t dq_workspace_elems,
+                                                const uint8_t* accumulate, void* stream);
+
+/*
+ * Block-schedule partial sum: out[i] = prev[i] + emitted[i] (FP32 arithmetic,
+ * stored as `dtype`, ATTNRES_DTYPE_F32 or ATTNRES_DTYPE_BF16) and
+ * out_bf16[i] = bf16(out[i]) (round to nearest even), for n_elems contiguous
+ * elements.  The running partial of a block and its BF16 copy for the next
+ * read in one pass, instead of an add, then a conversion inside the read's
+ * caller.  Replaces the caller step `partial_value = partial_value + emitted`
+ * followed by the read's BF16 cast (reference benchmarks/model.py:333 and
+ * :279-291).
+ */
+int attnres_hip_partial_sum(const void* prev, const void* emitted, int dtype,
+                            int64_t n_elems, void* out, void* out_bf16, void* stream);
 
 #ifdef __cplusplus
 }

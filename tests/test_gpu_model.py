@@ -99,3 +99,22 @@ def test_source_bank_model_matches_the_plain_model():
     (b * weight).sum().backward()
     for (name, p), q in zip(plain.named_parameters(), banked.parameters()):
         assert _relative_error(q.grad, p.grad) < 2e-2, name
+
+
+@pytest.mark.parametrize("blocks", [2, 3])
+def test_block_source_bank_model_matches_the_plain_model(blocks):
+    config = TrainingConfig(layers=3, width=64, heads=4, ffn=128, batch=2, sequence=32, vocab=97,
+                            block_count=blocks, mode="block", source_layout="packed", variant="standard")
+    torch.manual_seed(53)
+    plain = make_model(config, backend="kernel").cuda()
+    banked = make_model(config, backend="kernel", source_bank=True).cuda()
+    banked.load_state_dict(plain.state_dict())
+    tokens = torch.randint(config.vocab, (config.batch, config.sequence), device="cuda")
+    print(f"block bank model blocks={blocks}", flush=True)
+    a, b = plain(tokens), banked(tokens)
+    assert torch.equal(a, b)
+    weight = torch.randn_like(a)
+    (a * weight).sum().backward()
+    (b * weight).sum().backward()
+    for (name, p), q in zip(plain.named_parameters(), banked.parameters()):
+        assert _relative_error(q.grad, p.grad) < 2e-2, name

@@ -45,9 +45,9 @@ def test_config_rules():
     with pytest.raises(ValueError):
         make_model(_tiny(), backend="other")
     with pytest.raises(ValueError, match="source_bank"):
-        make_model(_tiny(mode="block"), source_bank=True)
-    with pytest.raises(ValueError, match="source_bank"):
         make_model(_tiny(), backend=oracle, source_bank=True)
+    with pytest.raises(ValueError, match="source_bank"):
+        make_model(_tiny(mode="block"), backend=oracle, source_bank=True)
 
 
 def test_block_ends():

@@ -20,7 +20,7 @@ _C_TYPES = {
     "const float*": ctypes.c_void_p, "int8_t*": ctypes.c_void_p, "const int8_t*": ctypes.c_void_p,
     "const void* const*": ctypes.c_void_p, "void* const*": ctypes.c_void_p,
     "const int64_t*": ctypes.c_void_p, "const uint8_t*": ctypes.c_void_p, "int64_t": ctypes.c_int64,
-    "float": ctypes.c_float,
+    "float": ctypes.c_float, "float* const*": ctypes.c_void_p, "int": ctypes.c_int,
 }
 
 
@@ -184,3 +184,29 @@ def test_backward_without_the_refinement_is_for_small_reads_only():
     status = lib.attnres_hip_packed_backward_accumulate(
         _FAKE, 64, 64, 3, 4, 64, _FAKE, 16, 1.0, None, None, _FAKE, *stats, _FAKE, _FAKE, _FAKE, need, flags, None)
     assert status == _native.ERR_NULL_POINTER
+
+
+def test_partial_sum_checks_its_arguments_on_the_host():
+    lib = _native.load()
+    assert lib.attnres_hip_partial_sum(None, _FAKE, 0, 16, _FAKE, _FAKE, None) == _native.ERR_NULL_POINTER
+    assert lib.attnres_hip_partial_sum(_FAKE, _FAKE, 2, 16, _FAKE, _FAKE, None) == _native.ERR_SHAPE
+    assert b"dtype" in lib.attnres_hip_last_error()
+    assert lib.attnres_hip_partial_sum(_FAKE, _FAKE, 0, 0, _FAKE, _FAKE, None) == _native.ERR_SHAPE
+    text = HEADER.read_text()
+    assert "#define ATTNRES_DTYPE_F32 0" in text and "#define ATTNRES_DTYPE_BF16 1" in text
+
+
+def test_list_f32_accumulating_backward_checks_like_the_others():
+    lib = _native.load()
+    need = lib.attnres_hip_dq_workspace_elems(4, 64, 16)
+    pointers = (ctypes.c_void_p * 3)(_FAKE, _FAKE, _FAKE)
+    strides = (ctypes.c_int64 * 3)(64, 64, 64)
+    flags = (ctypes.c_uint8 * 3)(0, 1, 0)
+    common = (_FAKE, 16, 1.0, _FAKE, _FAKE, _FAKE, _FAKE, _FAKE, _FAKE)
+    status = lib.attnres_hip_sources_backward_accumulate_f32(
+        pointers, strides, 3, 4, 64, *common, pointers, _FAKE, _FAKE, need, None, None)
+    assert status == _native.ERR_NULL_POINTER
+    assert b"accumulate_f32" in lib.attnres_hip_last_error()
+    status = lib.attnres_hip_sources_backward_accumulate_f32(
+        pointers, strides, 3, 4, 64, *common, pointers, _FAKE, _FAKE, need - 1, flags, None)
+    assert status == _native.ERR_WORKSPACE
