@@ -437,8 +437,9 @@ def read_sources_per_step(config) -> list[int]:
 def run_model(cfg: dict, steps: int, warmup: int, variant: str = "both") -> dict:
     """model / model_block: training steps of the causal LM (benchmarks/model.py).
 
-    ``variant`` "both" times the plain step (the line's value) and then the
-    source-bank step; "plain" or "bank" times one of them alone (for traces).
+    ``variant`` "both" times the plain step (the line's value), then the
+    source-bank step with gathered and with accumulated gradients; "plain",
+    "bank" or "bank_accumulate" times one of them alone (for traces).
     """
     import torch
 
@@ -453,9 +454,9 @@ def run_model(cfg: dict, steps: int, warmup: int, variant: str = "both") -> dict
     tokens = torch.randint(config.vocab, (config.batch, config.sequence), device="cuda", generator=generator)
     targets = torch.roll(tokens, -1, dims=1)
 
-    def time_steps(source_bank):
+    def time_steps(source_bank, bank_gradients="gather"):
         torch.manual_seed(0)
-        model = make_model(config, backend="kernel", source_bank=source_bank).cuda()
+        model = make_model(config, backend="kernel", source_bank=source_bank, bank_gradients=bank_gradients).cuda()
         optimizer = torch.optim.AdamW(model.parameters(), lr=1e-4)
         for _ in range(warmup):
             training_step(model, optimizer, tokens, targets)
@@ -468,8 +469,9 @@ def run_model(cfg: dict, steps: int, warmup: int, variant: str = "both") -> dict
         torch.cuda.synchronize()
         return start.elapsed_time(stop) / steps, float(loss)
 
-    ms, loss = time_steps(False) if variant != "bank" else (None, None)
-    bank_ms, bank_loss = time_steps(True) if variant != "plain" else (None, None)
+    ms, loss = time_steps(False) if variant in ("both", "plain") else (None, None)
+    bank_ms, bank_loss = time_steps(True) if variant in ("both", "bank") else (None, None)
+    acc_ms, acc_loss = time_steps(True, "accumulate") if variant in ("both", "bank_accumulate") else (None, None)
 
     def rate(t):
         return None if t is None else round(n_tokens / (t * 1e-3), 1)
@@ -498,6 +500,9 @@ def run_model(cfg: dict, steps: int, warmup: int, variant: str = "both") -> dict
         # fused partial sums)
         "source_bank": {"ms_per_step": rounded(bank_ms, 3), "tokens_per_s": rate(bank_ms),
                         "loss": rounded(bank_loss, 4)},
+        # the same with the bank's gradients summed in the backward kernels instead of gathered
+        "source_bank_accumulate": {"ms_per_step": rounded(acc_ms, 3), "tokens_per_s": rate(acc_ms),
+                                   "loss": rounded(acc_loss, 4)},
         "roofline": None,
         "cpu_baseline": None,
     }
@@ -512,8 +517,9 @@ def main(argv=None) -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU oracle time")
     parser.add_argument("--copy-probe", action="store_true")
-    parser.add_argument("--model-variant", choices=("both", "plain", "bank"), default="both",
-                        help="--config model: time the plain step, the source-bank step, or both")
+    parser.add_argument("--model-variant", choices=("both", "plain", "bank", "bank_accumulate"), default="both",
+                        help="--config model / model_block: time the plain step, the source-bank step (gathered "
+                             "or accumulated gradients), or all three")
     args = parser.parse_args(argv)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:

@@ -125,13 +125,17 @@ class TransformerLayer(nn.Module):
 class CausalAttnResLM(nn.Module):
     """Small causal Transformer with Full or Block AttnRes residual reads."""
 
-    def __init__(self, config: TrainingConfig, backend: Backend = "kernel", *, source_bank: bool = False) -> None:
+    def __init__(self, config: TrainingConfig, backend: Backend = "kernel", *, source_bank: bool = False,
+                 bank_gradients: str = "gather") -> None:
         super().__init__()
         if source_bank and backend != "kernel":
             raise ValueError("source_bank needs the HIP backend")
+        if bank_gradients not in ("gather", "accumulate"):
+            raise ValueError("bank_gradients must be 'gather' or 'accumulate'")
         self.config = config
         self.backend = backend
         self.source_bank = bool(source_bank)
+        self.bank_gradients = bank_gradients
         self.token_embedding = nn.Embedding(config.vocab, config.width)
         self.position_embedding = nn.Parameter(torch.empty(config.sequence, config.width))
         self.layers = nn.ModuleList(TransformerLayer(config) for _ in range(config.layers))
@@ -174,7 +178,7 @@ class CausalAttnResLM(nn.Module):
     def _forward_full_bank(self, embedded: Tensor) -> Tensor:
         from attnres import SourceBank
 
-        bank = SourceBank(2 * self.config.layers + 1)
+        bank = SourceBank(2 * self.config.layers + 1, gradients=self.bank_gradients)
         bank.push(embedded)
         for event in range(2 * self.config.layers):
             x = embedded if event == 0 else bank.read(self.queries[event - 1].to(torch.bfloat16)).to(embedded.dtype)
@@ -196,7 +200,7 @@ class CausalAttnResLM(nn.Module):
         events = 2 * self.config.layers
         ends = block_ends(events, self.config.block_count)
         # slots 0..len(ends): the embedding and the completed blocks; then one per mid-block partial
-        bank = SourceBank(len(ends) + 1 + events - len(ends))
+        bank = SourceBank(len(ends) + 1 + events - len(ends), gradients=self.bank_gradients)
         bank.push(embedded, slot=0)
         completed, scratch, event = 1, len(ends) + 1, 0
         for end in ends:
@@ -254,13 +258,15 @@ class CausalAttnResLM(nn.Module):
         return self.lm_head(hidden)
 
 
-def make_model(config: TrainingConfig, backend: Backend = "kernel", *, source_bank: bool = False) -> CausalAttnResLM:
-    """Construct a model with the given residual-read backend."""
+def make_model(config: TrainingConfig, backend: Backend = "kernel", *, source_bank: bool = False,
+               bank_gradients: str = "gather") -> CausalAttnResLM:
+    """Construct a model with the given residual-read backend (``bank_gradients``:
+    the source bank's gradient path, see ``attnres.SourceBank``)."""
     if not isinstance(config, TrainingConfig):
         raise TypeError("config must be a TrainingConfig")
     if not (backend == "kernel" or callable(backend)):
         raise ValueError("backend must be 'kernel' or a callable")
-    return CausalAttnResLM(config, backend, source_bank=source_bank)
+    return CausalAttnResLM(config, backend, source_bank=source_bank, bank_gradients=bank_gradients)
 
 
 def training_step(model: nn.Module, optimizer: torch.optim.Optimizer, tokens: Tensor, targets: Tensor,

@@ -45,6 +45,13 @@ from ._sources import _EPS, _MAX_SOURCES, _MAX_WIDTH, check_packed, check_source
 _DTYPE_F32, _DTYPE_BF16 = 0, 1  # attnres_hip.h ATTNRES_DTYPE_*
 
 
+class _GatherRead(ctypes.Structure):
+    """attnres_hip.h ``attnres_gather_read``."""
+
+    _fields_ = [("grad_out", ctypes.c_void_p), ("query_row", ctypes.c_void_p), ("coef", ctypes.c_void_p),
+                ("n_sources", ctypes.c_int64), ("position", ctypes.c_int64), ("rank", ctypes.c_int64)]
+
+
 def _pass_id() -> int:
     """The running backward pass: autograd's graph-task id (-1 outside one)."""
     return torch._C._current_graph_task_id()
@@ -179,20 +186,30 @@ class SourceBank:
     when a tail slot is added) with no per-read conversion or stack.
     ``push_sum`` adds the block's partial and the new output and writes the
     sum (in their dtype, returned) and its BF16 copy (into the slot) in one
-    kernel (``attnres_hip_partial_sum``).  In the backward every read adds its
-    FP32 dv into one FP32 ``[capacity, ..., D]`` buffer in the kernel
-    (``attnres_hip_{packed,sources}_backward_accumulate_f32``: the first
-    contribution to a slot writes it); slot i's sum is handed to its source
-    (in the source's dtype) once every read that saw slot i has run its
-    backward -- the slot's push node produced the token those reads take as
-    inputs.  The sums are FP32 without BF16 rounding of the per-read dv.
-    Eager mode only; one bank per forward pass.
+    kernel (``attnres_hip_partial_sum``).
+
+    Gradients (``gradients="gather"``, the default): a read's backward writes
+    no dv rows, only its dq and the per-token coefficients of its dv
+    (``attnres_hip_{packed,sources}_backward_coef``), and keeps its BF16 dO.
+    Slot i's gradient is formed once, when the slot's push node runs its
+    backward -- after every read that saw slot i, since those reads take the
+    node's token as an input -- by ``attnres_hip_bank_gather``: one FP32 pass
+    over the dO rows of those reads.  ``gradients="accumulate"`` instead adds
+    every read's FP32 dv into one FP32 ``[capacity, ..., D]`` buffer in the
+    backward kernel (``attnres_hip_{packed,sources}_backward_accumulate_f32``:
+    a read-modify-write of the sum per read).  Either way the sums are FP32
+    without BF16 rounding of the per-read dv, and reach the source in its
+    dtype.  Eager mode only; one bank per forward pass.
     """
 
-    def __init__(self, capacity: int) -> None:
+    def __init__(self, capacity: int, *, gradients: str = "gather") -> None:
         if isinstance(capacity, bool) or not isinstance(capacity, int) or not 1 <= capacity <= _MAX_SOURCES:
             raise ValueError(f"capacity must be an integer in 1..{_MAX_SOURCES}")
+        if gradients not in ("gather", "accumulate"):
+            raise ValueError("gradients must be 'gather' or 'accumulate'")
         self.capacity = capacity
+        self.gradients = gradients
+        self._pending: list[list[tuple[tuple, int]]] = [[] for _ in range(capacity)]
         self._values: Tensor | None = None
         self._tokens: list[Tensor | None] = [None] * capacity
         self._grads: Tensor | None = None
@@ -281,19 +298,24 @@ class SourceBank:
 
     def _backward(self, slots: tuple[int, ...], query: Tensor, out: Tensor, out_refine: Tensor, grad_out: Tensor,
                   logit: Tensor, inv_rms: Tensor, stats: Tensor, scale: float) -> Tensor:
+        current = _pass_id()
+        if self._pass != current:
+            # first read of this pass: nothing left from an earlier pass (one that stopped short
+            # of the sources) is used, and sums handed out earlier stay valid (fresh buffers)
+            self._grads = None
+            self._written = [False] * self.capacity
+            self._pending = [[] for _ in range(self.capacity)]
+            self._pass = current
+        if self.gradients == "gather":
+            return self._backward_coef(slots, query, out, out_refine, grad_out, logit, inv_rms, stats, scale)
         lib = _native.load()
         count = len(slots)
         width = int(self._values.shape[-1])
         tokens = self._values[0].numel() // width
         rank = query.numel()
         device = self._values.device
-        current = _pass_id()
-        if self._pass != current:
-            # first read of this pass: a fresh buffer, so sums handed out by an earlier pass
-            # (views of its buffer) stay valid and a pass that stopped short leaves nothing behind
+        if self._grads is None:
             self._grads = torch.empty(self._values.shape, device=device, dtype=torch.float32)
-            self._written = [False] * self.capacity
-            self._pass = current
         flags = (ctypes.c_uint8 * count)(*[1 if self._written[i] else 0 for i in slots])
         grad_query = torch.empty((rank,), device=device, dtype=torch.bfloat16)
         workspace = _dq_workspace(lib, tokens, width, rank, device)
@@ -318,12 +340,68 @@ class SourceBank:
             self._written[i] = True
         return grad_query
 
+    def _backward_coef(self, slots: tuple[int, ...], query: Tensor, out: Tensor, out_refine: Tensor,
+                       grad_out: Tensor, logit: Tensor, inv_rms: Tensor, stats: Tensor, scale: float) -> Tensor:
+        """First stage of the gathered gradients: dq and the dv coefficients now;
+        the read's dO and coefficients are kept for the slots' gathers."""
+        lib = _native.load()
+        count = len(slots)
+        width = int(self._values.shape[-1])
+        tokens = self._values[0].numel() // width
+        rank = query.numel()
+        device = self._values.device
+        grad_query = torch.empty((rank,), device=device, dtype=torch.bfloat16)
+        coef = torch.empty((3, count, tokens), device=device, dtype=torch.float32)
+        workspace = _dq_workspace(lib, tokens, width, rank, device)
+        grad_out = _contiguous(grad_out.to(torch.bfloat16))
+        saved = (_contiguous(out).data_ptr(), _contiguous(out_refine).data_ptr(), grad_out.data_ptr(),
+                 _contiguous(logit).data_ptr(), _contiguous(inv_rms).data_ptr(), _contiguous(stats).data_ptr())
+        with torch.cuda.device(device):
+            if self._prefix(slots):
+                status = lib.attnres_hip_packed_backward_coef(
+                    self._values.data_ptr(), tokens * width, width, count, tokens, width, query.data_ptr(), rank,
+                    scale, *saved, coef.data_ptr(), grad_query.data_ptr(), workspace.data_ptr(), workspace.numel(),
+                    _stream(device))
+            else:
+                pointers = (ctypes.c_void_p * count)(*[self._values[i].data_ptr() for i in slots])
+                strides = (ctypes.c_int64 * count)(*([width] * count))
+                status = lib.attnres_hip_sources_backward_coef(
+                    pointers, strides, count, tokens, width, query.data_ptr(), rank, scale, *saved, coef.data_ptr(),
+                    grad_query.data_ptr(), workspace.data_ptr(), workspace.numel(), _stream(device))
+        _native.check(status, "attnres source-bank coefficient backward")
+        query_row = torch.zeros((width,), device=device, dtype=torch.bfloat16)
+        query_row[width - rank:] = query.reshape(-1)
+        record = (grad_out, query_row, coef, count, rank)
+        for position, slot in enumerate(slots):
+            self._pending[slot].append((record, position))
+        return grad_query
+
     def _take(self, slot: int) -> Tensor | None:
-        """Slot `slot`'s FP32 sum (a view of this pass's buffer), or None."""
-        if self._pass != _pass_id() or not self._written[slot]:
+        """Slot `slot`'s FP32 gradient for this pass (gathered, or a view of the
+        accumulated sums), or None."""
+        if self._pass != _pass_id():
             return None
-        self._written[slot] = False
-        return self._grads[slot]
+        if self.gradients == "accumulate":
+            if not self._written[slot]:
+                return None
+            self._written[slot] = False
+            return self._grads[slot]
+        pending, self._pending[slot] = self._pending[slot], []
+        if not pending:
+            return None
+        lib = _native.load()
+        width = int(self._values.shape[-1])
+        tokens = self._values[0].numel() // width
+        reads = (_GatherRead * len(pending))()
+        for entry, ((grad_out, query_row, coef, count, rank), position) in zip(reads, pending):
+            entry.grad_out, entry.query_row, entry.coef = grad_out.data_ptr(), query_row.data_ptr(), coef.data_ptr()
+            entry.n_sources, entry.position, entry.rank = count, position, rank
+        grad = torch.empty(self._values.shape[1:], device=self._values.device, dtype=torch.float32)
+        with torch.cuda.device(self._values.device):
+            status = lib.attnres_hip_bank_gather(self._values[slot].data_ptr(), width, tokens, width, reads,
+                                                 len(pending), grad.data_ptr(), 0, _stream(self._values.device))
+        _native.check(status, "attnres source-bank gather")
+        return grad
 
 
 class _Push(torch.autograd.Function):

@@ -27,6 +27,7 @@ namespace attnres_hip {
 ATTNRES_FOR_EACH_GEOMETRY(ATTNRES_DECLARE_GEOMETRY)
 ATTNRES_FOR_EACH_GEOMETRY(ATTNRES_DECLARE_GEOMETRY_F32)
 ATTNRES_FOR_EACH_GEOMETRY(ATTNRES_DECLARE_GEOMETRY_RECOMPUTE)
+ATTNRES_FOR_EACH_GEOMETRY(ATTNRES_DECLARE_GEOMETRY_COEF)
 
 namespace {
 
@@ -256,10 +257,16 @@ int64_t launch_bwd_geometry_any(const BwdArgs<Rows, Grads>& a, bool nomask, bool
 template <int G, int CH, class Rows, class Grads>
 int64_t launch_bwd_select(const BwdArgs<Rows, Grads>& a, bool nomask, bool vec, bool acc, bool recompute,
                           hipStream_t stream) {
-  if constexpr (!kF32Grads<Grads>) {
-    if (recompute) return launch_bwd_recompute_geometry<G, CH>(a, nomask, vec, stream);
+  if constexpr (std::is_same_v<Grads, CoefSink>) {
+    (void)acc;
+    (void)recompute;
+    return launch_bwd_geometry_coef<G, CH>(a, nomask, vec, stream);
+  } else {
+    if constexpr (!kF32Grads<Grads>) {
+      if (recompute) return launch_bwd_recompute_geometry<G, CH>(a, nomask, vec, stream);
+    }
+    return launch_bwd_geometry_any<G, CH>(a, nomask, vec, acc, stream);
   }
-  return launch_bwd_geometry_any<G, CH>(a, nomask, vec, acc, stream);
 }
 
 template <class Rows, class Grads>
@@ -391,11 +398,13 @@ int packed_backward(const void* values, int64_t source_stride, int64_t row_strid
                     float* dq_workspace, int64_t dq_workspace_elems, const uint8_t* accumulate, bool need_flags,
                     void* stream) {
   constexpr bool kF32 = kF32Grads<Grads>;
-  const char* name = kF32 ? "attnres_hip_packed_backward_accumulate_f32"
+  constexpr bool kCoef = std::is_same_v<Grads, CoefSink>;
+  const char* name = kCoef ? "attnres_hip_packed_backward_coef"
+                     : kF32 ? "attnres_hip_packed_backward_accumulate_f32"
                      : need_flags ? "attnres_hip_packed_backward_accumulate" : "attnres_hip_packed_backward";
   int st = check_shape(n_sources, n_tokens, width, rank);
   if (st) return st;
-  const bool recompute = !need_flags && !out_refine;
+  const bool recompute = !kCoef && !need_flags && !out_refine;
   if (!values || !query || (!recompute && (!out || !out_refine)) || !grad_out || !logit || !inv_rms || !stats ||
       !grad_values || !grad_query || !dq_workspace || (need_flags && !accumulate))
     return fail(ATTNRES_ERR_NULL_POINTER, "null pointer argument to %s", name);
@@ -408,7 +417,9 @@ int packed_backward(const void* values, int64_t source_stride, int64_t row_strid
                 (long long)dq_workspace_elems, (long long)need);
   BwdArgs<PackedRows, Grads> a{};
   a.src = PackedRows{static_cast<const uint16_t*>(values), source_stride, row_stride};
-  if constexpr (kF32) {
+  if constexpr (kCoef) {
+    a.grad = CoefSink{static_cast<float*>(grad_values)};  // the coefficient planes
+  } else if constexpr (kF32) {
     a.grad = PackedGradsF32{static_cast<float*>(grad_values), n_tokens * width};
   } else {
     a.grad = PackedGrads{static_cast<uint16_t*>(grad_values), n_tokens * width};
@@ -427,7 +438,7 @@ int packed_backward(const void* values, int64_t source_stride, int64_t row_strid
   a.rank = static_cast<int>(rank);
   a.scale = scale;
   const bool vec = width % kVec == 0 && aligned16(values) && aligned16_or_null(out) &&
-                   aligned16_or_null(out_refine) && aligned16(grad_out) && aligned16(grad_values) &&
+                   aligned16_or_null(out_refine) && aligned16(grad_out) && (kCoef || aligned16(grad_values)) &&
                    (source_stride % kVec == 0 || n_sources == 1) && (row_stride % kVec == 0 || n_tokens == 1);
   const bool acc = set_accumulate(a, accumulate, n_sources);
   const int64_t rows = grid_blocks(n_tokens, width, 0);
@@ -525,15 +536,18 @@ int sources_backward(const void* const* sources, const int64_t* row_strides, int
                      const void* out, const int8_t* out_refine, const void* grad_out, const float* logit,
                      const float* inv_rms, const float* stats, void* const* grad_sources, void* grad_query,
                      float* dq_workspace, int64_t dq_workspace_elems, const uint8_t* accumulate, bool need_flags,
-                     void* stream) {
+                     void* stream, float* coef = nullptr) {
   constexpr bool kF32 = kF32Grads<Grads>;
-  const char* name = kF32 ? "attnres_hip_sources_backward_accumulate_f32"
+  constexpr bool kCoef = std::is_same_v<Grads, CoefSink>;
+  const char* name = kCoef ? "attnres_hip_sources_backward_coef"
+                     : kF32 ? "attnres_hip_sources_backward_accumulate_f32"
                      : need_flags ? "attnres_hip_sources_backward_accumulate" : "attnres_hip_sources_backward";
   int st = check_shape(n_sources, n_tokens, width, rank);
   if (st) return st;
-  const bool recompute = !need_flags && !out_refine;
+  const bool recompute = !kCoef && !need_flags && !out_refine;
   if (!sources || !row_strides || !query || (!recompute && (!out || !out_refine)) || !grad_out || !logit ||
-      !inv_rms || !stats || !grad_sources || !grad_query || !dq_workspace || (need_flags && !accumulate))
+      !inv_rms || !stats || (kCoef ? !coef : !grad_sources) || !grad_query || !dq_workspace ||
+      (need_flags && !accumulate))
     return fail(ATTNRES_ERR_NULL_POINTER, "null pointer argument to %s", name);
   if ((st = check_recompute(recompute, n_sources, name))) return st;
   if ((st = check_scalars(1.0f, scale, false))) return st;
@@ -544,15 +558,18 @@ int sources_backward(const void* const* sources, const int64_t* row_strides, int
   BwdArgs<ListRows, Grads> a{};
   bool vec = width % kVec == 0 && aligned16_or_null(out) && aligned16_or_null(out_refine) && aligned16(grad_out);
   for (int64_t s = 0; s < n_sources; ++s) {
-    if (!sources[s] || !grad_sources[s])
+    if (!sources[s] || (!kCoef && !grad_sources[s]))
       return fail(ATTNRES_ERR_NULL_POINTER, "source %lld or its gradient is null", (long long)s);
     if (row_strides[s] < 0) return fail(ATTNRES_ERR_STRIDE, "source %lld has a negative row stride", (long long)s);
     a.src.ptr[s] = static_cast<const uint16_t*>(sources[s]);
     a.src.row_stride[s] = row_strides[s];
-    a.grad.ptr[s] = static_cast<std::remove_reference_t<decltype(a.grad.ptr[0])>>(grad_sources[s]);
-    vec = vec && aligned16(sources[s]) && aligned16(grad_sources[s]) &&
-          (row_strides[s] % kVec == 0 || n_tokens == 1);
+    vec = vec && aligned16(sources[s]) && (row_strides[s] % kVec == 0 || n_tokens == 1);
+    if constexpr (!kCoef) {
+      a.grad.ptr[s] = static_cast<std::remove_reference_t<decltype(a.grad.ptr[0])>>(grad_sources[s]);
+      vec = vec && aligned16(grad_sources[s]);
+    }
   }
+  if constexpr (kCoef) a.grad.coef = coef;
   a.query = static_cast<const uint16_t*>(query);
   a.out = static_cast<const uint16_t*>(out);
   a.out_refine = out_refine;
@@ -616,6 +633,85 @@ int attnres_hip_sources_backward_accumulate_f32(const void* const* sources, cons
                                         out_refine, grad_out, logit, inv_rms, stats,
                                         reinterpret_cast<void* const*>(grad_sums), grad_query, dq_workspace,
                                         dq_workspace_elems, accumulate, true, stream);
+}
+
+int attnres_hip_packed_backward_coef(const void* values, int64_t source_stride, int64_t row_stride,
+                                     int64_t n_sources, int64_t n_tokens, int64_t width, const void* query,
+                                     int64_t rank, float scale, const void* out, const int8_t* out_refine,
+                                     const void* grad_out, const float* logit, const float* inv_rms,
+                                     const float* stats, float* coef, void* grad_query, float* dq_workspace,
+                                     int64_t dq_workspace_elems, void* stream) {
+  return packed_backward<CoefSink>(values, source_stride, row_stride, n_sources, n_tokens, width, query, rank, scale,
+                                   out, out_refine, grad_out, logit, inv_rms, stats, coef, grad_query, dq_workspace,
+                                   dq_workspace_elems, nullptr, false, stream);
+}
+
+int attnres_hip_sources_backward_coef(const void* const* sources, const int64_t* row_strides, int64_t n_sources,
+                                      int64_t n_tokens, int64_t width, const void* query, int64_t rank, float scale,
+                                      const void* out, const int8_t* out_refine, const void* grad_out,
+                                      const float* logit, const float* inv_rms, const float* stats, float* coef,
+                                      void* grad_query, float* dq_workspace, int64_t dq_workspace_elems,
+                                      void* stream) {
+  return sources_backward<CoefSink>(sources, row_strides, n_sources, n_tokens, width, query, rank, scale, out,
+                                    out_refine, grad_out, logit, inv_rms, stats, nullptr, grad_query, dq_workspace,
+                                    dq_workspace_elems, nullptr, false, stream, coef);
+}
+
+int attnres_hip_bank_gather(const void* values, int64_t row_stride, int64_t n_tokens, int64_t width,
+                            const attnres_gather_read* reads, int64_t n_reads, float* grad, int accumulate,
+                            void* stream) {
+  int st = check_shape(1, n_tokens, width, 1);
+  if (st) return st;
+  if (!values || !reads || !grad) return fail(ATTNRES_ERR_NULL_POINTER, "null pointer argument to attnres_hip_bank_gather");
+  if (row_stride < 0) return fail(ATTNRES_ERR_STRIDE, "negative row stride");
+  if (n_reads < 1) return fail(ATTNRES_ERR_SHAPE, "n_reads=%lld must be positive", (long long)n_reads);
+  bool vec = width % kVec == 0 && aligned16(values) && aligned16(grad) && (row_stride % kVec == 0 || n_tokens == 1);
+  for (int64_t r = 0; r < n_reads; ++r) {
+    const attnres_gather_read& rd = reads[r];
+    if (!rd.grad_out || !rd.query_row || !rd.coef)
+      return fail(ATTNRES_ERR_NULL_POINTER, "read %lld of attnres_hip_bank_gather has a null pointer", (long long)r);
+    if ((st = check_shape(rd.n_sources, n_tokens, width, rd.rank))) return st;
+    if (rd.position < 0 || rd.position >= rd.n_sources)
+      return fail(ATTNRES_ERR_SHAPE, "read %lld: position %lld outside 0..%lld", (long long)r,
+                  (long long)rd.position, (long long)rd.n_sources - 1);
+    vec = vec && aligned16(rd.grad_out) && aligned16(rd.query_row);
+  }
+  // One launch per run of at most kMaxGatherReads reads with the same rank
+  // (in the caller's order); every launch after the first adds to grad.
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const Geometry geo = geometry(width);
+  bool first_launch = true;
+  for (int64_t first = 0; first < n_reads;) {
+    GatherArgs a{};
+    a.values = static_cast<const uint16_t*>(values);
+    a.row_stride = row_stride;
+    a.grad = grad;
+    a.n_tokens = n_tokens;
+    a.width = static_cast<int>(width);
+    a.tail0 = static_cast<int>(width - reads[first].rank);
+    a.accumulate = (accumulate || !first_launch) ? 1 : 0;
+    int count = 0;
+    while (first + count < n_reads && count < kMaxGatherReads && reads[first + count].rank == reads[first].rank) {
+      const attnres_gather_read& rd = reads[first + count];
+      a.read[count++] = GatherRead{static_cast<const uint16_t*>(rd.grad_out),
+                                   static_cast<const uint16_t*>(rd.query_row), rd.coef + rd.position * n_tokens,
+                                   rd.n_sources * n_tokens};
+    }
+    a.n_reads = count;
+    switch (geo.lanes * 100 + geo.chunks) {
+      case 1601: launch_gather_geometry<16, 1>(a, vec, s); break;
+      case 3201: launch_gather_geometry<32, 1>(a, vec, s); break;
+      case 6401: launch_gather_geometry<64, 1>(a, vec, s); break;
+      case 6402: launch_gather_geometry<64, 2>(a, vec, s); break;
+      case 6404: launch_gather_geometry<64, 4>(a, vec, s); break;
+      case 6408: launch_gather_geometry<64, 8>(a, vec, s); break;
+      default: launch_gather_geometry<256, 4>(a, vec, s); break;
+    }
+    if ((st = launch_status("attnres bank gather")) != ATTNRES_OK) return st;
+    first += count;
+    first_launch = false;
+  }
+  return ATTNRES_OK;
 }
 
 int attnres_hip_partial_sum(const void* prev, const void* emitted, int dtype, int64_t n_elems, void* out,

@@ -83,6 +83,14 @@ struct ListGradsF32 {
   }
 };
 
+// The coefficient backward of a source bank writes, instead of dv rows, the
+// per-(token, source) terms of dv = p dO + a q + [key] b v as three FP32
+// planes [3, S, N] (p, a, b; tokens contiguous); the slots' gradients are
+// gathered later from the reads' dO rows.
+struct CoefSink {
+  float* coef;
+};
+
 // Gradient types whose rows are FP32 sums (written or added without rounding).
 template <class Grads>
 inline constexpr bool kF32Grads = false;
@@ -129,6 +137,30 @@ struct BwdArgs {
   // gradient that dv is added to (bf16(old + dv)); clear -> dv is written.
   uint64_t accumulate[(kMaxSources + 63) / 64];
   __host__ __device__ bool accumulates(int s) const { return (accumulate[s >> 6] >> (s & 63)) & 1u; }
+};
+
+// One read that saw the slot being gathered (see attnres_hip_bank_gather).
+constexpr int kMaxGatherReads = 48;  // per launch; more reads take further, accumulating launches
+struct GatherRead {
+  const uint16_t* grad_out;  // [N, D] BF16 dO of the read
+  const uint16_t* qrow;      // [D] BF16: the query on the read's key coordinates, 0 before them
+  const float* p;            // [N] plane of the read's coefficients for this slot (a, b follow
+                             // at plane_stride and 2 * plane_stride elements)
+  int64_t plane_stride;      // S_r * N
+};
+
+// The reads of one launch share their query length R (key coordinates
+// tail0 = D - R .. D-1), so their b v terms add up to one scalar per token.
+struct GatherArgs {
+  const uint16_t* values;  // the slot's [N, D] BF16 rows (row n at values + n * row_stride)
+  int64_t row_stride;
+  float* grad;             // [N, D] FP32, contiguous
+  int64_t n_tokens;
+  int width;
+  int tail0;
+  int n_reads;
+  int accumulate;          // 1: add to grad, 0: write it
+  GatherRead read[kMaxGatherReads];
 };
 
 // ------------------------------------------------------------------ geometry
@@ -197,6 +229,19 @@ int64_t launch_bwd_recompute_geometry(const BwdArgs<Rows, Grads>& a, bool nomask
       const BwdArgs<PackedRows, PackedGrads>&, bool, bool, hipStream_t);                        \
   extern template int64_t launch_bwd_recompute_geometry<G, CH, ListRows, ListGrads>(            \
       const BwdArgs<ListRows, ListGrads>&, bool, bool, hipStream_t);
+
+// The coefficient backward (dz instead of dv) and the slot gather.
+template <int G, int CH, class Rows>
+int64_t launch_bwd_geometry_coef(const BwdArgs<Rows, CoefSink>& a, bool nomask, bool vec, hipStream_t stream);
+template <int G, int CH>
+void launch_gather_geometry(const GatherArgs& a, bool vec, hipStream_t stream);
+
+#define ATTNRES_DECLARE_GEOMETRY_COEF(G, CH)                                                                 \
+  extern template int64_t launch_bwd_geometry_coef<G, CH, PackedRows>(const BwdArgs<PackedRows, CoefSink>&, \
+                                                                      bool, bool, hipStream_t);              \
+  extern template int64_t launch_bwd_geometry_coef<G, CH, ListRows>(const BwdArgs<ListRows, CoefSink>&,     \
+                                                                    bool, bool, hipStream_t);                \
+  extern template void launch_gather_geometry<G, CH>(const GatherArgs&, bool, hipStream_t);
 
 // The accumulating backward into FP32 gradient sums.
 template <int G, int CH, class Rows, class Grads>

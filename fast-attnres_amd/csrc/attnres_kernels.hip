@@ -671,7 +671,9 @@ struct GradRows {
 template <int G, int CH, int NB, bool NOMASK, bool VEC, bool ACC, class Rows, class Grads>
 __global__ void __launch_bounds__(kBlock) attnres_bwd_kernel(const BwdArgs<Rows, Grads> a) {
   constexpr bool kF32 = kF32Grads<Grads>;
+  constexpr bool kCoef = std::is_same_v<Grads, CoefSink>;
   static_assert(!kF32 || ACC, "FP32 gradient sums use the accumulating variant");
+  static_assert(!kCoef || !ACC, "the coefficient backward writes no gradient rows");
   static_assert(G <= 64 || G == kBlock, "a wide group is the whole workgroup");
   constexpr int kGroups = kBlock / G;
   __shared__ float xred[xred_floats<G>(1)];
@@ -788,6 +790,26 @@ __global__ void __launch_bounds__(kBlock) attnres_bwd_kernel(const BwdArgs<Rows,
       const float dz = p * (dw[0] - delta);
       const float ca = inv_rms * (dz * scale);                  // on q; dq += ca * key
       const float cb = -(inv_rms * inv_rms) * (dz * z * inv_R);  // on the key coordinates
+      if constexpr (kCoef) {
+        // coefficient backward: p, a, b for the later gather, dq here; no dv row
+        if (lane == 0) {
+          float* plane = a.grad.coef + static_cast<int64_t>(s) * a.n_tokens + token;
+          const int64_t stride = static_cast<int64_t>(S) * a.n_tokens;
+          plane[0] = p;
+          plane[stride] = ca;
+          plane[2 * stride] = cb;
+        }
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+          const uint32_t w[4] = {ring[j][c].x, ring[j][c].y, ring[j][c].z, ring[j][c].w};
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const uint32_t kw = NOMASK ? w[k] : (w[k] & km[c][k]);
+            dq[c][2 * k] = fmaf(ca, bf16_lo(kw), dq[c][2 * k]);
+            dq[c][2 * k + 1] = fmaf(ca, bf16_hi(kw), dq[c][2 * k + 1]);
+          }
+        }
+      } else {
       auto* grad_row = a.grad.row(s, token, D);
       // dO is unpacked per item with a shift and mask the compiler cannot
       // prove loop-invariant (s >= 0, so both equal the constants): a hoisted
@@ -845,6 +867,7 @@ __global__ void __launch_bounds__(kBlock) attnres_bwd_kernel(const BwdArgs<Rows,
           store_chunk<VEC>(grad_row, d0, D, u32x4{out[0], out[1], out[2], out[3]});
         }
       }
+      }  // kCoef
 
       if (refill) {
         __builtin_amdgcn_sched_barrier(0);  // refill the slot after its last use
@@ -992,6 +1015,126 @@ __global__ void __launch_bounds__(kBlock) attnres_bwd_recompute_kernel(const Bwd
   store_dq_partial<G, CH>(dq, dq_lds, a.partial + static_cast<int64_t>(blockIdx.x) * R, group, lane, tail0, D);
 }
 
+// ---------------------------------------------------------- source-bank gather
+
+// The gradient of one source-bank slot, gathered from the reads that saw it:
+//   grad[n] = sum_r ( p_r dO_r[n] + a_r q_r ) + [key] (sum_r b_r) v[n]
+// with p, a, b of read r at token n as its coefficient backward wrote them --
+// the same terms as the read's own dv, summed over the reads in FP32 in one
+// pass instead of one read-modify-write of an FP32 sum per read.  The reads
+// of a launch share R, so the b terms meet in one scalar per token.
+// A group takes T consecutive tokens at a time (grid-stride over token
+// blocks), so each read's query row is loaded once per T tokens and its
+// coefficients for the T tokens are contiguous.  A ring of kRing reads keeps
+// the next reads' rows in flight while one is added.
+template <int G, int CH, bool VEC>
+__global__ void __launch_bounds__(kBlock) attnres_gather_kernel(const GatherArgs a) {
+  static_assert(kBlock % G == 0 && (G <= 64 || G % 64 == 0), "groups of whole wavefronts above 64 lanes");
+  constexpr int T = CH >= 4 ? 1 : 4 / CH;      // tokens per group iteration
+  constexpr int kRing = 2;                     // reads in flight per group (T rows each)
+  constexpr int kGroups = kBlock / G;
+  const int lane = threadIdx.x % G;
+  const int group = group_index<G>();
+  const int D = a.width;
+  const int64_t N = a.n_tokens;
+  const int n_reads = a.n_reads;
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * kGroups + group;
+  const int64_t groups = static_cast<int64_t>(gridDim.x) * kGroups;
+  const int64_t blocks = (N + T - 1) / T;
+  for (int64_t blk = gid; blk < blocks; blk += groups) {
+    const int64_t token0 = blk * T;
+    int64_t tok[T];  // clamped: a block past N re-reads the last token and stores nothing for it
+#pragma unroll
+    for (int t = 0; t < T; ++t) tok[t] = token0 + t < N ? token0 + t : N - 1;
+    float acc[T][CH][kVec];
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int c = 0; c < CH; ++c)
+#pragma unroll
+        for (int e = 0; e < kVec; ++e) acc[t][c][e] = 0.0f;
+    float bsum[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) bsum[t] = 0.0f;
+    u32x4 g[kRing][T][CH], q[kRing][CH];
+    float cp[kRing][T], ca[kRing][T], cb[kRing][T];
+    auto request = [&](int b, int r) __attribute__((always_inline)) {
+      const GatherRead& rd = a.read[r < n_reads ? r : n_reads - 1];  // past the end: the last read again
+      load_row<G, CH, VEC>(rd.qrow, lane, D, q[b]);
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        load_row<G, CH, VEC>(rd.grad_out + tok[t] * D, lane, D, g[b][t]);
+        cp[b][t] = rd.p[tok[t]];
+        ca[b][t] = rd.p[rd.plane_stride + tok[t]];
+        cb[b][t] = rd.p[2 * rd.plane_stride + tok[t]];
+      }
+    };
+    auto add = [&](int b) __attribute__((always_inline)) {
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        bsum[t] += cb[b][t];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+          const uint32_t gw[4] = {g[b][t][c].x, g[b][t][c].y, g[b][t][c].z, g[b][t][c].w};
+          const uint32_t qw[4] = {q[b][c].x, q[b][c].y, q[b][c].z, q[b][c].w};
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            acc[t][c][2 * k] = fmaf(ca[b][t], bf16_lo(qw[k]), fmaf(cp[b][t], bf16_lo(gw[k]), acc[t][c][2 * k]));
+            acc[t][c][2 * k + 1] =
+                fmaf(ca[b][t], bf16_hi(qw[k]), fmaf(cp[b][t], bf16_hi(gw[k]), acc[t][c][2 * k + 1]));
+          }
+        }
+      }
+    };
+#pragma unroll
+    for (int j = 0; j < kRing; ++j) request(j, j);
+    for (int r = 0; r < n_reads; r += kRing) {
+#pragma unroll
+      for (int j = 0; j < kRing; ++j) {
+        if (r + j < n_reads) add(j);        // uniform
+        __builtin_amdgcn_sched_barrier(0);  // refill the slot after its use
+        request(j, r + j + kRing);
+      }
+    }
+    // the key terms, then the earlier sum (accumulate) and the store
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      if (token0 + t >= N) break;  // uniform
+      u32x4 v[CH];
+      load_row<G, CH, VEC>(a.values + tok[t] * a.row_stride, lane, D, v);
+      float* grad_row = a.grad + tok[t] * D;
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const int d0 = chunk_start<G>(c, lane);
+        const uint32_t vw[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int d = d0 + 2 * k;
+          acc[t][c][2 * k] = fmaf(d >= a.tail0 ? bsum[t] : 0.0f, bf16_lo(vw[k]), acc[t][c][2 * k]);
+          acc[t][c][2 * k + 1] = fmaf(d + 1 >= a.tail0 ? bsum[t] : 0.0f, bf16_hi(vw[k]), acc[t][c][2 * k + 1]);
+        }
+        if (a.accumulate) {  // uniform
+#pragma unroll
+          for (int e = 0; e < kVec; ++e) acc[t][c][e] += grad_row[min(d0 + e, D - 1)];
+        }
+        if constexpr (VEC) {
+          if (d0 < D) {
+            __builtin_nontemporal_store(f32x4{acc[t][c][0], acc[t][c][1], acc[t][c][2], acc[t][c][3]},
+                                        reinterpret_cast<f32x4*>(grad_row + d0));
+            __builtin_nontemporal_store(f32x4{acc[t][c][4], acc[t][c][5], acc[t][c][6], acc[t][c][7]},
+                                        reinterpret_cast<f32x4*>(grad_row + d0 + 4));
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < kVec; ++e) {
+            if (d0 + e < D) grad_row[d0 + e] = acc[t][c][e];
+          }
+        }
+      }
+    }
+  }
+}
+
 // ----------------------------------------------------------------- launchers
 
 // Ring depth (rows in flight per group) for a chunk count.  Measured on
@@ -1114,6 +1257,32 @@ int64_t launch_bwd_geometry_f32(const BwdArgs<Rows, Grads>& a, bool nomask, bool
   return launch_bwd_variant<G, CH, true>(a, nomask, vec, stream);
 }
 
+template <int G, int CH, class Rows>
+int64_t launch_bwd_geometry_coef(const BwdArgs<Rows, CoefSink>& a, bool nomask, bool vec, hipStream_t stream) {
+  return launch_bwd_variant<G, CH, false>(a, nomask, vec, stream);
+}
+
+// The gather has no group sums, so a row is spread over up to a whole
+// workgroup with as few chunks per lane as the width allows (fewer registers:
+// 64 lanes x 4 chunks took 204 VGPRs, 256 x 1 far fewer).
+template <int G, int CH>
+void launch_gather_geometry(const GatherArgs& a, bool vec, hipStream_t stream) {
+  constexpr int kLanes = G * CH <= kBlock ? G * CH : kBlock;
+  constexpr int kChunks = G * CH / kLanes;
+  static_assert(kLanes * kChunks == G * CH, "same row coverage");
+  if (vec) {
+    const int64_t blocks =
+        grid_blocks(a.n_tokens, a.width, resident_blocks<&attnres_gather_kernel<kLanes, kChunks, true>>());
+    hipLaunchKernelGGL((attnres_gather_kernel<kLanes, kChunks, true>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(kBlock), 0, stream, a);
+  } else {
+    const int64_t blocks =
+        grid_blocks(a.n_tokens, a.width, resident_blocks<&attnres_gather_kernel<kLanes, kChunks, false>>());
+    hipLaunchKernelGGL((attnres_gather_kernel<kLanes, kChunks, false>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(kBlock), 0, stream, a);
+  }
+}
+
 #if defined(ATTNRES_LANES) && defined(ATTNRES_CHUNKS)
 template void launch_fwd_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, PackedRows>(const FwdArgs<PackedRows>&, bool,
                                                                              bool, hipStream_t);
@@ -1127,6 +1296,11 @@ template int64_t launch_bwd_geometry_f32<ATTNRES_LANES, ATTNRES_CHUNKS, PackedRo
     const BwdArgs<PackedRows, PackedGradsF32>&, bool, bool, hipStream_t);
 template int64_t launch_bwd_geometry_f32<ATTNRES_LANES, ATTNRES_CHUNKS, ListRows, ListGradsF32>(
     const BwdArgs<ListRows, ListGradsF32>&, bool, bool, hipStream_t);
+template int64_t launch_bwd_geometry_coef<ATTNRES_LANES, ATTNRES_CHUNKS, PackedRows>(
+    const BwdArgs<PackedRows, CoefSink>&, bool, bool, hipStream_t);
+template int64_t launch_bwd_geometry_coef<ATTNRES_LANES, ATTNRES_CHUNKS, ListRows>(const BwdArgs<ListRows, CoefSink>&,
+                                                                                   bool, bool, hipStream_t);
+template void launch_gather_geometry<ATTNRES_LANES, ATTNRES_CHUNKS>(const GatherArgs&, bool, hipStream_t);
 template int64_t launch_bwd_recompute_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, PackedRows, PackedGrads>(
     const BwdArgs<PackedRows, PackedGrads>&, bool, bool, hipStream_t);
 template int64_t launch_bwd_recompute_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, ListRows, ListGrads>(

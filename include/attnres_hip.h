@@ -258,6 +258,62 @@ int attnres_hip_sources_backward_accumulate_f32(const void* const* sources,
                                                 const uint8_t* accumulate, void* stream);
 
 /*
+ * Coefficient backward (a source bank's first backward stage): the same
+ * arguments as attnres_hip_packed_backward / attnres_hip_sources_backward
+ * (out and out_refine required), but instead of gradient rows it writes
+ * coef[3, S, N] (FP32, contiguous): for token n and source s the terms of
+ * dv = p dO + a q + b v (b on the key coordinates), i.e.
+ *   p = exp(z - max) / sum,  a = inv_rms * scale * dz,  b = -inv_rms^2 * dz * z / R,
+ *   dz = p (<v, dO> - <dO, o>);
+ * dq is written as usual.  The source gradients are formed later, per source,
+ * by attnres_hip_bank_gather from the dO and coefficients of every read that
+ * saw it.  No counterpart in the reference; used by attnres.SourceBank.
+ */
+int attnres_hip_packed_backward_coef(const void* values, int64_t source_stride,
+                                     int64_t row_stride, int64_t n_sources,
+                                     int64_t n_tokens, int64_t width,
+                                     const void* query, int64_t rank, float scale,
+                                     const void* out, const int8_t* out_refine,
+                                     const void* grad_out, const float* logit,
+                                     const float* inv_rms, const float* stats, float* coef,
+                                     void* grad_query, float* dq_workspace,
+                                     int64_t dq_workspace_elems, void* stream);
+
+int attnres_hip_sources_backward_coef(const void* const* sources,
+                                      const int64_t* row_strides, int64_t n_sources,
+                                      int64_t n_tokens, int64_t width,
+                                      const void* query, int64_t rank, float scale,
+                                      const void* out, const int8_t* out_refine,
+                                      const void* grad_out, const float* logit,
+                                      const float* inv_rms, const float* stats, float* coef,
+                                      void* grad_query, float* dq_workspace,
+                                      int64_t dq_workspace_elems, void* stream);
+
+/* One read that saw the gathered source (attnres_hip_bank_gather). */
+typedef struct attnres_gather_read {
+  const void* grad_out;   /* [N, D] BF16, contiguous: the read's upstream gradient     */
+  const void* query_row;  /* [D] BF16: its query on the last `rank` coordinates, 0 before */
+  const float* coef;      /* [3, n_sources, N] from the read's coefficient backward   */
+  int64_t n_sources;      /* the read's source count                                  */
+  int64_t position;       /* the gathered source's position in the read's list        */
+  int64_t rank;           /* the read's query length R                                */
+} attnres_gather_read;
+
+/*
+ * Gradient of one source from every read that saw it (HOST array `reads`):
+ *   grad[n] (+)= sum_r p_r dO_r[n] + a_r q_r + b_r v[n]   (b_r on r's key coordinates)
+ * with p, a, b of read r at token n from its coefficient backward -- the
+ * read's own dv, summed over the reads in FP32.
+ * `values` are the source's BF16 rows (row n at values + n*row_stride), grad
+ * is contiguous FP32 [N, D]; accumulate != 0 adds to it.  One pass over the
+ * dO rows instead of one read-modify-write of an FP32 sum per read.  No
+ * counterpart in the reference; used by attnres.SourceBank.
+ */
+int attnres_hip_bank_gather(const void* values, int64_t row_stride, int64_t n_tokens,
+                            int64_t width, const attnres_gather_read* reads,
+                            int64_t n_reads, float* grad, int accumulate, void* stream);
+
+/*
  * Block-schedule partial sum: out[i] = prev[i] + emitted[i] (FP32 arithmetic,
  * stored as `dtype`, ATTNRES_DTYPE_F32 or ATTNRES_DTYPE_BF16) and
  * out_bf16[i] = bf16(out[i]) (round to nearest even), for n_elems contiguous

@@ -112,13 +112,14 @@ def _run_stream(read, push, embedded, weights, queries):
     return outs
 
 
+@pytest.mark.parametrize("gradients", ["gather", "accumulate"])
 @pytest.mark.parametrize("width,rank", [(512, 512), (1024, 128)], ids=["d512_r512", "d1024_r128"])
-def test_source_bank_matches_the_plain_stream_and_the_oracle(width, rank):
+def test_source_bank_matches_the_plain_stream_and_the_oracle(width, rank, gradients):
     from attnres import SourceBank
 
     embedded, weights, queries, grads = _stream_case(width, rank)
-    print(f"source bank width={width} rank={rank}", flush=True)
-    bank = SourceBank(len(weights) + 1)
+    print(f"source bank width={width} rank={rank} gradients={gradients}", flush=True)
+    bank = SourceBank(len(weights) + 1, gradients=gradients)
     outs_bank = _run_stream(lambda q: bank.read(q.to(torch.bfloat16)).float(), bank.push, embedded, weights, queries)
     sources = []
     outs_ref = _run_stream(
@@ -201,7 +202,8 @@ def test_push_sum_is_the_add_and_the_cast(shape, dtype):
     assert torch.equal(gp, grad) and torch.equal(ge, grad)
 
 
-def test_source_bank_tail_reads_match_attnres():
+@pytest.mark.parametrize("gradients", ["gather", "accumulate"])
+def test_source_bank_tail_reads_match_attnres(gradients):
     """Block-style reads (completed slots plus a partial in a tail slot)
     against attnres over the same BF16 sources: outputs and dq identical,
     source gradients equal to autograd's sums within BF16 rounding."""
@@ -218,7 +220,7 @@ def test_source_bank_tail_reads_match_attnres():
     def run(bank_mode):
         outs = []
         if bank_mode:
-            bank = SourceBank(6)
+            bank = SourceBank(6, gradients=gradients)
             for i, block in enumerate(blocks):
                 bank.push(block, slot=i)
             bank.push(emitted[0], slot=3)
@@ -239,7 +241,7 @@ def test_source_bank_tail_reads_match_attnres():
         params = (*blocks, *emitted, *queries)
         return outs, torch.autograd.grad(outs, params, grads)
 
-    print("source bank tail reads", flush=True)
+    print(f"source bank tail reads gradients={gradients}", flush=True)
     outs_bank, g_bank = run(True)
     outs_ref, g_ref = run(False)
     for a, b in zip(outs_bank, outs_ref):
@@ -253,3 +255,25 @@ def test_source_bank_tail_reads_match_attnres():
             assert float((a.float() - b.float()).norm() / b.float().norm()) < 2e-3
     for a, b in zip(g_bank[:-4], g_ref[:-4]):
         torch.testing.assert_close(a, b, rtol=2.0**-6, atol=2.0**-6 * float(b.abs().max()))
+
+
+def test_gather_matches_accumulate_over_many_reads():
+    """A slot read by more reads than one gather launch takes (48), with two
+    query lengths among them: the gathered gradients equal the accumulated
+    ones to FP32 rounding."""
+    from attnres import SourceBank
+
+    torch.manual_seed(59)
+    width, tokens, reads = 512, (67,), 53
+    sources = [torch.randn(*tokens, width, device="cuda", requires_grad=True) for _ in range(3)]
+    queries = [(torch.randn(width if r % 3 else 128, device="cuda") / 8).to(torch.bfloat16) for r in range(reads)]
+    grads = [torch.randn(*tokens, width, device="cuda") for _ in range(reads)]
+    results = {}
+    for mode in ("gather", "accumulate"):
+        bank = SourceBank(3, gradients=mode)
+        for source in sources:
+            bank.push(source)
+        outs = [bank.read(q, count=1 + r % 3).float() for r, q in enumerate(queries)]
+        results[mode] = torch.autograd.grad(outs, sources, grads)
+    for a, b in zip(results["gather"], results["accumulate"]):
+        torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-5 * float(b.abs().max()))

@@ -21,6 +21,7 @@ _C_TYPES = {
     "const void* const*": ctypes.c_void_p, "void* const*": ctypes.c_void_p,
     "const int64_t*": ctypes.c_void_p, "const uint8_t*": ctypes.c_void_p, "int64_t": ctypes.c_int64,
     "float": ctypes.c_float, "float* const*": ctypes.c_void_p, "int": ctypes.c_int,
+    "const attnres_gather_read*": ctypes.c_void_p,
 }
 
 
@@ -210,3 +211,44 @@ def test_list_f32_accumulating_backward_checks_like_the_others():
     status = lib.attnres_hip_sources_backward_accumulate_f32(
         pointers, strides, 3, 4, 64, *common, pointers, _FAKE, _FAKE, need - 1, flags, None)
     assert status == _native.ERR_WORKSPACE
+
+
+def test_gather_read_struct_matches_the_header():
+    """attnres_gather_read: three pointers and three int64, in the header's
+    order (the ctypes mirror attnres.shared._GatherRead)."""
+    from attnres.shared import _GatherRead
+
+    body = re.search(r"typedef struct attnres_gather_read \{(.*?)\} attnres_gather_read;", HEADER.read_text(), re.S)
+    fields = re.findall(r"^\s*[\w\s\*]+?\b(\w+);", re.sub(r"/\*.*?\*/", "", body.group(1), flags=re.S), re.M)
+    assert fields == [name for name, _ in _GatherRead._fields_]
+    assert ctypes.sizeof(_GatherRead) == 6 * 8
+
+
+def test_coefficient_backward_and_gather_check_on_the_host():
+    from attnres.shared import _GatherRead
+
+    lib = _native.load()
+    need = lib.attnres_hip_dq_workspace_elems(4, 64, 16)
+    stats = (_FAKE, _FAKE, _FAKE)
+    status = lib.attnres_hip_packed_backward_coef(
+        _FAKE, 64, 64, 3, 4, 64, _FAKE, 16, 1.0, _FAKE, None, _FAKE, *stats, _FAKE, _FAKE, _FAKE, need, None)
+    assert status == _native.ERR_NULL_POINTER  # the coefficient backward needs the saved refinement
+    status = lib.attnres_hip_packed_backward_coef(
+        _FAKE, 64, 64, 3, 4, 64, _FAKE, 16, 1.0, _FAKE, _FAKE, _FAKE, *stats, None, _FAKE, _FAKE, need, None)
+    assert status == _native.ERR_NULL_POINTER
+    pointers = (ctypes.c_void_p * 3)(_FAKE, _FAKE, _FAKE)
+    strides = (ctypes.c_int64 * 3)(64, 64, 64)
+    status = lib.attnres_hip_sources_backward_coef(
+        pointers, strides, 3, 4, 64, _FAKE, 16, 1.0, _FAKE, _FAKE, _FAKE, *stats, _FAKE, _FAKE, _FAKE, need - 1,
+        None)
+    assert status == _native.ERR_WORKSPACE
+    reads = (_GatherRead * 2)()
+    for entry in reads:
+        entry.grad_out = entry.query_row = entry.coef = _FAKE
+        entry.n_sources, entry.position, entry.rank = 3, 1, 16
+    reads[1].position = 3
+    assert lib.attnres_hip_bank_gather(_FAKE, 64, 4, 64, reads, 2, _FAKE, 0, None) == _native.ERR_SHAPE
+    assert b"position" in lib.attnres_hip_last_error()
+    reads[1].position, reads[1].coef = 2, None
+    assert lib.attnres_hip_bank_gather(_FAKE, 64, 4, 64, reads, 2, _FAKE, 0, None) == _native.ERR_NULL_POINTER
+    assert lib.attnres_hip_bank_gather(_FAKE, 64, 4, 64, reads, 0, _FAKE, 0, None) == _native.ERR_SHAPE
