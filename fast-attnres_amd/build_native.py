@@ -32,7 +32,7 @@ OUTPUT = HERE / "attnres" / "_lib" / "libattnres_hip.so"
 ARCH = "gfx950"
 # (lanes, chunks) per translation unit; must match ATTNRES_FOR_EACH_GEOMETRY
 # in csrc/attnres_internal.h.
-GEOMETRIES = ((16, 1), (32, 1), (64, 1), (64, 2), (64, 4), (64, 8), (256, 4))
+GEOMETRIES = ((16, 1), (32, 1), (32, 2), (32, 4), (64, 4), (64, 8), (256, 4))
 FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 

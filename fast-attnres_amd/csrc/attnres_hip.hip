@@ -232,8 +232,8 @@ int launch_forward(const FwdArgs<Rows>& a, bool vec, hipStream_t stream) {
   switch (geo.lanes * 100 + geo.chunks) {
     case 1601: launch_fwd_geometry<16, 1>(a, nomask, vec, stream); break;
     case 3201: launch_fwd_geometry<32, 1>(a, nomask, vec, stream); break;
-    case 6401: launch_fwd_geometry<64, 1>(a, nomask, vec, stream); break;
-    case 6402: launch_fwd_geometry<64, 2>(a, nomask, vec, stream); break;
+    case 3202: launch_fwd_geometry<32, 2>(a, nomask, vec, stream); break;
+    case 3204: launch_fwd_geometry<32, 4>(a, nomask, vec, stream); break;
     case 6404: launch_fwd_geometry<64, 4>(a, nomask, vec, stream); break;
     case 6408: launch_fwd_geometry<64, 8>(a, nomask, vec, stream); break;
     default: launch_fwd_geometry<256, 4>(a, nomask, vec, stream); break;
@@ -278,8 +278,8 @@ int launch_backward(const BwdArgs<Rows, Grads>& a, bool vec, bool acc, bool reco
   switch (geo.lanes * 100 + geo.chunks) {
     case 1601: blocks = launch_bwd_select<16, 1>(a, nomask, vec, acc, recompute, stream); break;
     case 3201: blocks = launch_bwd_select<32, 1>(a, nomask, vec, acc, recompute, stream); break;
-    case 6401: blocks = launch_bwd_select<64, 1>(a, nomask, vec, acc, recompute, stream); break;
-    case 6402: blocks = launch_bwd_select<64, 2>(a, nomask, vec, acc, recompute, stream); break;
+    case 3202: blocks = launch_bwd_select<32, 2>(a, nomask, vec, acc, recompute, stream); break;
+    case 3204: blocks = launch_bwd_select<32, 4>(a, nomask, vec, acc, recompute, stream); break;
     case 6404: blocks = launch_bwd_select<64, 4>(a, nomask, vec, acc, recompute, stream); break;
     case 6408: blocks = launch_bwd_select<64, 8>(a, nomask, vec, acc, recompute, stream); break;
     default: blocks = launch_bwd_select<256, 4>(a, nomask, vec, acc, recompute, stream); break;
@@ -701,8 +701,8 @@ int attnres_hip_bank_gather(const void* values, int64_t row_stride, int64_t n_to
     switch (geo.lanes * 100 + geo.chunks) {
       case 1601: launch_gather_geometry<16, 1>(a, vec, s); break;
       case 3201: launch_gather_geometry<32, 1>(a, vec, s); break;
-      case 6401: launch_gather_geometry<64, 1>(a, vec, s); break;
-      case 6402: launch_gather_geometry<64, 2>(a, vec, s); break;
+      case 3202: launch_gather_geometry<32, 2>(a, vec, s); break;
+      case 3204: launch_gather_geometry<32, 4>(a, vec, s); break;
       case 6404: launch_gather_geometry<64, 4>(a, vec, s); break;
       case 6408: launch_gather_geometry<64, 8>(a, vec, s); break;
       default: launch_gather_geometry<256, 4>(a, vec, s); break;

@@ -170,13 +170,19 @@ struct Geometry {
   int chunks;  // 16-byte chunks per lane
 };
 
-// The smallest group that covers D: 16/32/64 lanes (one or several tokens per
+// Row geometry: 16/32/64 lanes per token (one or several tokens per
 // wavefront, no barriers) up to D = 4096, one workgroup per token beyond.
+// From D = 257 to 1024 a token takes 32 lanes with 2 or 4 chunks (two tokens
+// per wavefront) rather than 64 lanes with 1 or 2: each item's group sum
+// then covers twice the bytes.  Measured on MI355X at N = 16384, fwd + bwd:
+// D = 1024, S = 9: 200 -> 190 us, S = 25: 490 -> 458, S = 48: 918 -> 885;
+// D = 512, S = 25: 264 -> 255.  At D = 2048, 32 x 8 is no faster than 64 x 4
+// (it runs at occupancy 1).
 inline Geometry geometry(int64_t D) {
   if (D <= 16 * kVec) return {16, 1};
   if (D <= 32 * kVec) return {32, 1};
-  if (D <= 64 * kVec) return {64, 1};
-  if (D <= 128 * kVec) return {64, 2};
+  if (D <= 64 * kVec) return {32, 2};
+  if (D <= 128 * kVec) return {32, 4};
   if (D <= 256 * kVec) return {64, 4};
   if (D <= 512 * kVec) return {64, 8};
   return {256, 4};
@@ -253,7 +259,7 @@ int64_t launch_bwd_geometry_f32(const BwdArgs<Rows, Grads>& a, bool nomask, bool
   extern template int64_t launch_bwd_geometry_f32<G, CH, ListRows, ListGradsF32>(                 \
       const BwdArgs<ListRows, ListGradsF32>&, bool, bool, hipStream_t);
 
-#define ATTNRES_FOR_EACH_GEOMETRY(X) X(16, 1) X(32, 1) X(64, 1) X(64, 2) X(64, 4) X(64, 8) X(256, 4)
+#define ATTNRES_FOR_EACH_GEOMETRY(X) X(16, 1) X(32, 1) X(32, 2) X(32, 4) X(64, 4) X(64, 8) X(256, 4)
 
 }  // namespace attnres_hip
 
