@@ -173,6 +173,85 @@ def cpu_baseline(values, query, grad_out, budget_s: float, chunk: int) -> dict:
     }
 
 
+def graph_replay(values, query, grad_out, cfg: dict, replays: int, rounds: int = 5) -> dict:
+    """fwd+bwd of one packed read through the C ABI, captured into a HIP graph
+    and replayed: the reference harness's "cuda_graph" boundary (an event
+    interval around fixed graph replays, benchmarks/run.py:590-599), i.e. the
+    kernels' time without host or launch gaps.  Best of `rounds`."""
+    import ctypes
+    import re
+
+    import torch
+
+    from attnres import _native
+
+    lib = _native.load()
+    loaded = sorted(set(re.findall(r"\S*libamdhip64\.so\S*", open("/proc/self/maps").read())))
+    hip = ctypes.CDLL(loaded[0])  # the runtime torch already loaded
+    vp, i32 = ctypes.c_void_p, ctypes.c_int
+    for name, args in {"hipStreamBeginCapture": [vp, i32], "hipStreamEndCapture": [vp, ctypes.POINTER(vp)],
+                       "hipGraphInstantiate": [ctypes.POINTER(vp), vp, vp, vp, ctypes.c_size_t],
+                       "hipGraphLaunch": [vp, vp], "hipGraphExecDestroy": [vp], "hipGraphDestroy": [vp]}.items():
+        fn = getattr(hip, name)
+        fn.restype, fn.argtypes = i32, args
+    S, width, rank = cfg["sources"], cfg["width"], cfg["rank"]
+    packed = values.detach().reshape(S, -1, width)
+    N = packed.shape[1]
+    dev = packed.device
+    out = torch.empty(N, width, device=dev, dtype=torch.bfloat16)
+    refine = torch.empty(N if S > 3 else 0, width, device=dev, dtype=torch.int8)
+    logit, inv_rms = torch.empty(N, S, device=dev), torch.empty(N, S, device=dev)
+    stats = torch.empty(2, N, device=dev)
+    dv = torch.empty_like(packed)
+    dq = torch.empty(rank, device=dev, dtype=torch.bfloat16)
+    ws = torch.empty(lib.attnres_hip_dq_workspace_elems(N, width, rank), device=dev)
+    g = grad_out.reshape(N, width)
+    refine_ptr = refine.data_ptr() if refine.numel() else None
+    stream = torch.cuda.Stream()
+
+    def enqueue():
+        h = stream.cuda_stream
+        st = lib.attnres_hip_packed_forward(packed.data_ptr(), N * width, width, S, N, width, query.data_ptr(), rank,
+                                            2.0**-23, 1.0, out.data_ptr(), refine_ptr, logit.data_ptr(),
+                                            inv_rms.data_ptr(), stats.data_ptr(), h)
+        st = st or lib.attnres_hip_packed_backward(
+            packed.data_ptr(), N * width, width, S, N, width, query.data_ptr(), rank, 1.0,
+            out.data_ptr() if refine_ptr else None, refine_ptr, g.data_ptr(), logit.data_ptr(), inv_rms.data_ptr(),
+            stats.data_ptr(), dv.data_ptr(), dq.data_ptr(), ws.data_ptr(), ws.numel(), h)
+        _native.check(st, "graph-replay read")
+
+    stream.wait_stream(torch.cuda.current_stream())
+    enqueue()  # eager first: the library's per-thread launch caches are filled outside capture
+    torch.cuda.synchronize()
+    graph, exe = vp(), vp()
+    assert hip.hipStreamBeginCapture(vp(stream.cuda_stream), 2) == 0  # relaxed
+    enqueue()
+    assert hip.hipStreamEndCapture(vp(stream.cuda_stream), ctypes.byref(graph)) == 0
+    assert hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0) == 0
+    try:
+        times = []
+        for round_index in range(rounds + 1):  # round 0 warms up
+            start, stop = _event(), _event()
+            with torch.cuda.stream(stream):
+                start.record()
+                for _ in range(replays):
+                    assert hip.hipGraphLaunch(exe, vp(stream.cuda_stream)) == 0
+                stop.record()
+            torch.cuda.synchronize()
+            if round_index:
+                times.append(start.elapsed_time(stop) / replays)
+        best = min(times)
+        fwd_bytes, bwd_bytes = read_bytes(S, N, width)
+        tbs = (fwd_bytes + bwd_bytes) / (best * 1e-3) / 1e12
+        return {"us_per_read": round(best * 1e3, 2), "TB/s": round(tbs, 4),
+                "pct_of_peak": round(100 * tbs / HBM_PEAK_TBS, 2), "replays": replays, "rounds": rounds,
+                "boundary": "HIP events around back-to-back replays of a graph holding the C-ABI forward and "
+                            "backward (reference harness cuda_graph boundary); best round"}
+    finally:
+        hip.hipGraphExecDestroy(exe)
+        hip.hipGraphDestroy(graph)
+
+
 def _event():
     import torch
 
@@ -626,6 +705,8 @@ def main(argv=None) -> int:
                      "traffic": measured_traffic(args.config, "backward_bytes")},
         "cpu_baseline": None,
     }
+    # the same read through the C ABI, captured into a HIP graph and replayed
+    record["graph_replay"] = graph_replay(values, query, grad_out, cfg, replays=max(args.steps // 5, 4))
     if not args.no_cpu_baseline:
         record["cpu_baseline"] = cpu_baseline(values.detach(), query.detach(), grad_out,
                                               args.cpu_budget, chunk=2048)
