@@ -23,7 +23,7 @@ from helpers import SEEDS, compare, oracle_grads
 
 pytestmark = pytest.mark.gpu
 
-# (width, rank): geometry (lanes, chunks) -- 16x1 masked, 32x1, 64x1, 64x2 masked,
+# (width, rank): geometry (lanes, chunks) -- 16x1 masked, 32x1, 32x2, 32x4 masked,
 # 64x4, 64x8 (run as 256x2) with and without masks, 256x4 with and without masks
 WIDTHS = [(128, 40), (256, 256), (512, 512), (1000, 96), (2048, 2048), (3000, 257), (4096, 4096),
           (6144, 1024), (8192, 8192)]
