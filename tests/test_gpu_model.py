@@ -118,3 +118,25 @@ def test_block_source_bank_model_matches_the_plain_model(blocks):
     (b * weight).sum().backward()
     for (name, p), q in zip(plain.named_parameters(), banked.parameters()):
         assert _relative_error(q.grad, p.grad) < 2e-2, name
+
+
+@pytest.mark.parametrize("mode", ["full", "block"])
+def test_inductor_compiled_model_step_matches_eager(mode):
+    """The default torch.compile backend (inductor) around the whole model,
+    fullgraph: the reads stay opaque custom ops between inductor's fused
+    kernels; logits and parameter gradients match the eager model."""
+    config = _config(mode, "packed", "standard")
+    print(f"inductor model mode={mode}", flush=True)
+    torch.manual_seed(61)
+    eager = make_model(config, backend="kernel").cuda()
+    compiled_model = copy.deepcopy(eager)
+    tokens = torch.randint(config.vocab, (config.batch, config.sequence), device="cuda")
+    torch._dynamo.reset()
+    compiled = torch.compile(compiled_model, fullgraph=True)
+    a = eager(tokens)
+    b = compiled(tokens)
+    torch.testing.assert_close(b, a, rtol=1e-4, atol=1e-5)
+    a.float().square().mean().backward()
+    b.float().square().mean().backward()
+    for (name, p), q in zip(eager.named_parameters(), compiled_model.parameters()):
+        assert _relative_error(q.grad, p.grad) < 1e-2, name
