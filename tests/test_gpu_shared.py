@@ -277,3 +277,57 @@ def test_gather_matches_accumulate_over_many_reads():
         results[mode] = torch.autograd.grad(outs, sources, grads)
     for a, b in zip(results["gather"], results["accumulate"]):
         torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-5 * float(b.abs().max()))
+
+
+def test_source_bank_rejects_misuse():
+    from attnres import SourceBank
+
+    width = 64
+    a = torch.randn(3, width, device="cuda")
+    bank = SourceBank(4)
+    assert bank.push(a) == 0 and len(bank) == 1
+    with pytest.raises(ValueError, match="already holds"):
+        bank.push(a, slot=0)
+    with pytest.raises(ValueError, match="slot must be"):
+        bank.push(a, slot=4)
+    with pytest.raises(ValueError, match="same logical shape"):
+        bank.push(torch.randn(2, width, device="cuda"))
+    with pytest.raises(TypeError, match="floating-point"):
+        bank.push(torch.ones(3, width, device="cuda", dtype=torch.int32))
+    query = torch.randn(width, device="cuda", dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="pushed slots"):
+        bank.read(query, count=2)  # slot 1 is empty
+    bank.push(a, slot=2)
+    with pytest.raises(ValueError, match="needs count"):
+        bank.read(query, tail=2)
+    with pytest.raises(ValueError, match="tail must be"):
+        bank.read(query, count=1, tail=3)  # not pushed
+    with pytest.raises(ValueError, match="push_sum needs"):
+        bank.push_sum(a, a.double(), slot=3)
+    with pytest.raises(TypeError, match="float32 and bfloat16"):
+        bank.push_sum(a.half(), a.half(), slot=3)
+    out = bank.read(query, count=1, tail=2)  # slots 0 and 2
+    assert out.shape == (3, width) and out.dtype == torch.bfloat16
+    with pytest.raises(ValueError, match="gradients must be"):
+        SourceBank(2, gradients="sum")
+
+
+def test_source_bank_source_also_used_outside_the_bank():
+    """A pushed source that also feeds other ops gets both gradients summed by autograd."""
+    from attnres import SourceBank
+
+    torch.manual_seed(67)
+    width, rank = 256, 64
+    x = torch.randn(5, width, device="cuda", requires_grad=True)
+    y = torch.randn(5, width, device="cuda", requires_grad=True)
+    query = (torch.randn(rank, device="cuda") / 8).to(torch.bfloat16)
+    for mode in ("gather", "accumulate"):
+        bank = SourceBank(2, gradients=mode)
+        bank.push(x)
+        bank.push(y)
+        loss = (bank.read(query).float() * 3).sum() + (x * x).sum()
+        gx, gy = torch.autograd.grad(loss, (x, y))
+        ref = attnres(torch.stack([x.to(torch.bfloat16), y.to(torch.bfloat16)]), query)
+        rx, ry = torch.autograd.grad((ref.float() * 3).sum() + (x * x).sum(), (x, y))
+        torch.testing.assert_close(gx, rx, rtol=2.0**-6, atol=2.0**-6 * float(rx.abs().max()))
+        torch.testing.assert_close(gy, ry, rtol=2.0**-6, atol=2.0**-6 * float(ry.abs().max()))
