@@ -517,8 +517,10 @@ def run_model(cfg: dict, steps: int, warmup: int, variant: str = "both") -> dict
     """model / model_block: training steps of the causal LM (benchmarks/model.py).
 
     ``variant`` "both" times the plain step (the line's value), then the
-    source-bank step with gathered and with accumulated gradients; "plain",
-    "bank" or "bank_accumulate" times one of them alone (for traces).
+    source-bank step with gathered gradients, with accumulated gradients and
+    with inductor-compiled sublayers; "plain", "bank", "bank_accumulate" or
+    "bank_compiled" times one of them alone (for traces), "compiled" the plain
+    model under whole-model inductor compilation.
     """
     import torch
 
@@ -533,9 +535,10 @@ def run_model(cfg: dict, steps: int, warmup: int, variant: str = "both") -> dict
     tokens = torch.randint(config.vocab, (config.batch, config.sequence), device="cuda", generator=generator)
     targets = torch.roll(tokens, -1, dims=1)
 
-    def time_steps(source_bank, bank_gradients="gather", compiled=False):
+    def time_steps(source_bank, bank_gradients="gather", compiled=False, compile_layers=False):
         torch.manual_seed(0)
-        model = make_model(config, backend="kernel", source_bank=source_bank, bank_gradients=bank_gradients).cuda()
+        model = make_model(config, backend="kernel", source_bank=source_bank, bank_gradients=bank_gradients,
+                           compile_layers=compile_layers).cuda()
         optimizer = torch.optim.AdamW(model.parameters(), lr=1e-4)
         if compiled:  # inductor around the model; the reads stay opaque custom ops
             torch._dynamo.reset()
@@ -555,6 +558,8 @@ def run_model(cfg: dict, steps: int, warmup: int, variant: str = "both") -> dict
     bank_ms, bank_loss = time_steps(True) if variant in ("both", "bank") else (None, None)
     acc_ms, acc_loss = time_steps(True, "accumulate") if variant in ("both", "bank_accumulate") else (None, None)
     comp_ms, comp_loss = time_steps(False, compiled=True) if variant == "compiled" else (None, None)
+    bc_ms, bc_loss = (time_steps(True, compile_layers=True) if variant in ("both", "bank_compiled")
+                      else (None, None))
 
     def rate(t):
         return None if t is None else round(n_tokens / (t * 1e-3), 1)
@@ -586,6 +591,9 @@ def run_model(cfg: dict, steps: int, warmup: int, variant: str = "both") -> dict
         # the same with the bank's gradients summed in the backward kernels instead of gathered
         "source_bank_accumulate": {"ms_per_step": rounded(acc_ms, 3), "tokens_per_s": rate(acc_ms),
                                    "loss": rounded(acc_loss, 4)},
+        # the source-bank step with each sublayer compiled by inductor (regional compilation)
+        "source_bank_compiled_layers": {"ms_per_step": rounded(bc_ms, 3), "tokens_per_s": rate(bc_ms),
+                                        "loss": rounded(bc_loss, 4)},
         # --model-variant compiled: the plain model under torch.compile(fullgraph=True) (inductor)
         "compiled": {"ms_per_step": rounded(comp_ms, 3), "tokens_per_s": rate(comp_ms), "loss": rounded(comp_loss, 4)},
         "roofline": None,
@@ -602,10 +610,12 @@ def main(argv=None) -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU oracle time")
     parser.add_argument("--copy-probe", action="store_true")
-    parser.add_argument("--model-variant", choices=("both", "plain", "bank", "bank_accumulate", "compiled"),
+    parser.add_argument("--model-variant",
+                        choices=("both", "plain", "bank", "bank_accumulate", "bank_compiled", "compiled"),
                         default="both",
                         help="--config model / model_block: time the plain step, the source-bank step (gathered "
-                             "or accumulated gradients), all three (both), or the plain model under inductor")
+                             "or accumulated gradients, or with compiled sublayers), all four (both), or the plain "
+                             "model under inductor")
     args = parser.parse_args(argv)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:

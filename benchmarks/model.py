@@ -126,7 +126,7 @@ class CausalAttnResLM(nn.Module):
     """Small causal Transformer with Full or Block AttnRes residual reads."""
 
     def __init__(self, config: TrainingConfig, backend: Backend = "kernel", *, source_bank: bool = False,
-                 bank_gradients: str = "gather") -> None:
+                 bank_gradients: str = "gather", compile_layers: bool = False) -> None:
         super().__init__()
         if source_bank and backend != "kernel":
             raise ValueError("source_bank needs the HIP backend")
@@ -143,6 +143,12 @@ class CausalAttnResLM(nn.Module):
         # one query per read: before sublayers 2 .. 2L and before the LM head
         self.queries = nn.ParameterList(nn.Parameter(torch.empty(config.rank)) for _ in range(2 * config.layers))
         self.reset_parameters()
+        if compile_layers:
+            # regional compilation: each sublayer fused by inductor, while the residual stream
+            # (reads, source bank) between them stays eager
+            for layer in self.layers:
+                layer.attention = torch.compile(layer.attention, fullgraph=True)
+                layer.mlp = torch.compile(layer.mlp, fullgraph=True)
 
     def reset_parameters(self) -> None:
         for module in self.modules():
@@ -259,14 +265,16 @@ class CausalAttnResLM(nn.Module):
 
 
 def make_model(config: TrainingConfig, backend: Backend = "kernel", *, source_bank: bool = False,
-               bank_gradients: str = "gather") -> CausalAttnResLM:
+               bank_gradients: str = "gather", compile_layers: bool = False) -> CausalAttnResLM:
     """Construct a model with the given residual-read backend (``bank_gradients``:
-    the source bank's gradient path, see ``attnres.SourceBank``)."""
+    the source bank's gradient path, see ``attnres.SourceBank``; ``compile_layers``:
+    each attention and MLP sublayer under ``torch.compile(fullgraph=True)``)."""
     if not isinstance(config, TrainingConfig):
         raise TypeError("config must be a TrainingConfig")
     if not (backend == "kernel" or callable(backend)):
         raise ValueError("backend must be 'kernel' or a callable")
-    return CausalAttnResLM(config, backend, source_bank=source_bank, bank_gradients=bank_gradients)
+    return CausalAttnResLM(config, backend, source_bank=source_bank, bank_gradients=bank_gradients,
+                           compile_layers=compile_layers)
 
 
 def training_step(model: nn.Module, optimizer: torch.optim.Optimizer, tokens: Tensor, targets: Tensor,
