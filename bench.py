@@ -513,7 +513,7 @@ def read_sources_per_step(config) -> list[int]:
     return counts + [completed]
 
 
-def run_model(cfg: dict, steps: int, warmup: int, variant: str = "both") -> dict:
+def run_model(cfg: dict, steps: int, warmup: int, variant: str = "both", autocast: bool = False) -> dict:
     """model / model_block: training steps of the causal LM (benchmarks/model.py).
 
     ``variant`` "both" times the plain step (the line's value), then the
@@ -543,13 +543,16 @@ def run_model(cfg: dict, steps: int, warmup: int, variant: str = "both") -> dict
         if compiled:  # inductor around the model; the reads stay opaque custom ops
             torch._dynamo.reset()
             model = torch.compile(model, fullgraph=True)
-        for _ in range(warmup):
-            training_step(model, optimizer, tokens, targets)
+        context = torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast)
+        with context:
+            for _ in range(warmup):
+                training_step(model, optimizer, tokens, targets)
         torch.cuda.synchronize()
         start, stop = _event(), _event()
         start.record()
-        for _ in range(steps):
-            loss = training_step(model, optimizer, tokens, targets)
+        with context:
+            for _ in range(steps):
+                loss = training_step(model, optimizer, tokens, targets)
         stop.record()
         torch.cuda.synchronize()
         return start.elapsed_time(stop) / steps, float(loss)
@@ -576,10 +579,12 @@ def run_model(cfg: dict, steps: int, warmup: int, variant: str = "both") -> dict
                   f"S={min(counts)}..{max(counts)}), tokens/s",
         "value": rate(ms), "unit": "tokens/s", "n_gpus": 1, "steps": steps,
         "warmup": warmup, "ms_per_step": rounded(ms, 3), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "f32 model, bf16 reads", "data": "synthetic tokens (seeded)",
+        "vs_baseline": None, "dtype": "bf16 autocast" if autocast else "f32 model, bf16 reads",
+        "data": "synthetic tokens (seeded)",
         "config": {"workload": cfg["name"], "layers": config.layers, "width": config.width, "heads": config.heads,
                    "ffn": config.ffn, "batch": config.batch, "sequence": config.sequence, "vocab": config.vocab,
                    "mode": config.mode, "block_count": config.block_count if config.mode == "block" else None,
+                   "autocast": "bf16" if autocast else "off",
                    "reads_per_step": reads, "read_sources": counts,
                    "attnres_algorithmic_bytes_per_step": read_bytes_per_step},
         "loss": rounded(loss, 4),
@@ -610,6 +615,9 @@ def main(argv=None) -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU oracle time")
     parser.add_argument("--copy-probe", action="store_true")
+    parser.add_argument("--autocast", choices=("off", "bf16"), default="off",
+                        help="--config model / model_block: run the steps under torch.autocast (BF16), as the "
+                             "reference's 24-layer timings do")
     parser.add_argument("--model-variant",
                         choices=("both", "plain", "bank", "bank_accumulate", "bank_compiled", "compiled"),
                         default="both",
@@ -640,7 +648,7 @@ def main(argv=None) -> int:
     if args.config in ("c4", "c5", "model", "model_block", "policy"):
         torch.cuda.set_device(0)
         if args.config in ("model", "model_block"):
-            result = run_model(cfg, args.steps, args.warmup, args.model_variant)
+            result = run_model(cfg, args.steps, args.warmup, args.model_variant, args.autocast == "bf16")
         else:
             run = {"c4": run_block_schedule, "c5": run_sweep, "policy": run_policy}[args.config]
             result = run(cfg, args.steps, args.warmup)

@@ -15,7 +15,9 @@ read ``attnres(sources, query_i)`` with one learned query per read.
 
 The surrounding Transformer is ordinary PyTorch in the model's dtype; reads
 cast their sources to BF16 and their output back (reference `_read`,
-model.py:279-291).  ``backend`` is ``"kernel"`` (the HIP operator) or any
+model.py:279-291).  Under ``torch.autocast`` the embedding is cast to the
+autocast dtype (reference model.py:243-244), so with BF16 autocast the whole
+residual stream is BF16 and those casts are no-ops.  ``backend`` is ``"kernel"`` (the HIP operator) or any
 callable with the ``attnres`` signature, e.g. the CPU oracle for parity tests.
 
 ``source_bank=True`` (HIP backend; no reference counterpart) keeps the
@@ -260,6 +262,8 @@ class CausalAttnResLM(nn.Module):
         if tokens.shape[1] > self.config.sequence:
             raise ValueError("token sequence exceeds configured sequence length")
         embedded = self.token_embedding(tokens) + self.position_embedding[: tokens.shape[1]]
+        if torch.is_autocast_enabled(embedded.device.type):  # the stream in the autocast dtype (model.py:243-244)
+            embedded = embedded.to(torch.get_autocast_dtype(embedded.device.type))
         hidden = self._forward_full(embedded) if self.config.mode == "full" else self._forward_block(embedded)
         return self.lm_head(hidden)
 

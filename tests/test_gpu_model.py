@@ -161,3 +161,31 @@ def test_bank_model_with_compiled_sublayers_matches_eager(mode):
     b.float().square().mean().backward()
     for (name, p), q in zip(eager.named_parameters(), compiled.parameters()):
         assert _relative_error(q.grad, p.grad) < 2e-2, name
+
+
+@pytest.mark.parametrize("mode", ["full", "block"])
+def test_bf16_autocast_model_with_and_without_the_bank(mode):
+    """Under BF16 autocast the residual stream is BF16 (the embedding is cast,
+    reference model.py:243-244): the plain and the source-bank model give the
+    same logits, close gradients, and a few training steps reduce the loss."""
+    config = _config(mode, "packed", "standard")
+    print(f"bf16 autocast model mode={mode}", flush=True)
+    torch.manual_seed(73)
+    plain = make_model(config, backend="kernel").cuda()
+    banked = make_model(config, backend="kernel", source_bank=True).cuda()
+    banked.load_state_dict(plain.state_dict())
+    tokens = torch.randint(config.vocab, (config.batch, config.sequence), device="cuda")
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        a, b = plain(tokens), banked(tokens)
+        assert a.dtype == torch.bfloat16
+        assert torch.equal(a, b)
+        weight = torch.randn_like(a, dtype=torch.float32)
+        (a.float() * weight).sum().backward()
+        (b.float() * weight).sum().backward()
+    for (name, p), q in zip(plain.named_parameters(), banked.parameters()):
+        assert _relative_error(q.grad, p.grad) < 3e-2, name
+    optimizer = torch.optim.AdamW(banked.parameters(), lr=3e-3)
+    targets = torch.roll(tokens, -1, dims=1)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        losses = [float(training_step(banked, optimizer, tokens, targets)) for _ in range(8)]
+    assert losses[-1] < losses[0]
