@@ -38,6 +38,15 @@
 // one partial row, and two small kernels sum the partial rows in a fixed
 // order, so dq is bit-reproducible run to run.
 //
+// Variants of the backward.  For S <= 3 (the save/recompute policy) a group
+// holds all S rows of its token and takes delta = sum_s p_s dw_s from them,
+// so the forward stores no refinement and the backward reads no saved output
+// (attnres_bwd_recompute_kernel).  The accumulating variant adds dv to
+// existing gradient rows (BF16, or FP32 sums for a source bank).  The
+// coefficient variant writes no dv at all, only the per-token terms p, a, b;
+// a source bank later forms each source's gradient once from the dO rows of
+// every read that saw it (attnres_gather_kernel).
+//
 // Reference behaviour followed: src/attnres/_kernels/fixed_tail.py:244-483
 // (forward), :485-873 (backward), :875-899 (dq reduction); the list layout of
 // src/attnres/_kernels/fla_full_sources.py:164-214, 297-629.
