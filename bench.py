@@ -77,6 +77,10 @@ CONFIGS = {
                    name="save/recompute policy: reads of S=1..3 at N=16384, D in {1024,2048,4096}, R=D, packed"),
     "model": dict(layers=24, width=1024, heads=16, ffn=2816, batch=16, sequence=1024, vocab=8192,
                   name="24-layer Full-schedule causal LM training step, D=1024, 16x1024 tokens, FP32 outside the reads"),
+    "model_ref": dict(layers=24, width=1024, heads=16, ffn=2816, batch=2, sequence=1024, vocab=32768, autocast=True,
+                      fused_adamw=True,
+                      name="the reference's 24-layer workload (docs/current_24l_results.md): Full schedule, "
+                           "L24 D1024 H16 FFN2816 vocab 32768, B2 x T1024, BF16 autocast, fused AdamW"),
     "model_block": dict(layers=24, width=1024, heads=16, ffn=2816, batch=16, sequence=1024, vocab=8192, block_count=8,
                         name="24-layer Block-schedule (8 blocks) causal LM training step, D=1024, 16x1024 tokens, "
                              "FP32 outside the reads"),
@@ -514,14 +518,16 @@ def read_sources_per_step(config) -> list[int]:
 
 
 def run_model(cfg: dict, steps: int, warmup: int, variant: str = "both", autocast: bool = False) -> dict:
-    """model / model_block: training steps of the causal LM (benchmarks/model.py).
+    """model / model_block / model_ref: training steps of the causal LM (benchmarks/model.py).
 
     ``variant`` "both" times the plain step (the line's value), then the
     source-bank step with gathered gradients, with accumulated gradients and
     with inductor-compiled sublayers; "plain", "bank", "bank_accumulate" or
     "bank_compiled" times one of them alone (for traces), "compiled" the plain
-    model under whole-model inductor compilation.
+    model under whole-model inductor compilation. A config with "autocast"
+    always runs under BF16 autocast.
     """
+    autocast = autocast or cfg.get("autocast", False)
     import torch
 
     from benchmarks.model import TrainingConfig, make_model, training_step
@@ -539,20 +545,24 @@ def run_model(cfg: dict, steps: int, warmup: int, variant: str = "both", autocas
         torch.manual_seed(0)
         model = make_model(config, backend="kernel", source_bank=source_bank, bank_gradients=bank_gradients,
                            compile_layers=compile_layers).cuda()
-        optimizer = torch.optim.AdamW(model.parameters(), lr=1e-4)
+        optimizer = torch.optim.AdamW(model.parameters(), lr=1e-4, fused=cfg.get("fused_adamw", False))
         if compiled:  # inductor around the model; the reads stay opaque custom ops
             torch._dynamo.reset()
             model = torch.compile(model, fullgraph=True)
-        context = torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast)
-        with context:
-            for _ in range(warmup):
-                training_step(model, optimizer, tokens, targets)
+        def step():
+            # autocast is entered per step, as the reference's loop does (examples/train.py:45):
+            # it keeps its BF16 weight casts until the context exits, so one context around
+            # several steps would reuse the first step's casts of weights the optimizer changed
+            with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+                return training_step(model, optimizer, tokens, targets)
+
+        for _ in range(warmup):
+            step()
         torch.cuda.synchronize()
         start, stop = _event(), _event()
         start.record()
-        with context:
-            for _ in range(steps):
-                loss = training_step(model, optimizer, tokens, targets)
+        for _ in range(steps):
+            loss = step()
         stop.record()
         torch.cuda.synchronize()
         return start.elapsed_time(stop) / steps, float(loss)
@@ -645,9 +655,9 @@ def main(argv=None) -> int:
 
     _native.load()  # fail loudly if the HIP library is missing
     cfg = CONFIGS[args.config]
-    if args.config in ("c4", "c5", "model", "model_block", "policy"):
+    if args.config in ("c4", "c5", "model", "model_block", "model_ref", "policy"):
         torch.cuda.set_device(0)
-        if args.config in ("model", "model_block"):
+        if args.config in ("model", "model_block", "model_ref"):
             result = run_model(cfg, args.steps, args.warmup, args.model_variant, args.autocast == "bf16")
         else:
             run = {"c4": run_block_schedule, "c5": run_sweep, "policy": run_policy}[args.config]

@@ -106,4 +106,21 @@ def check_sources(values, query, eps, scale) -> tuple[tuple[torch.Tensor, ...], 
     return sources, eps_value, scale_value
 
 
-__all__ = ["check_packed", "check_scalar", "check_sources"]
+def check_query(query, width: int, device: torch.device, eps, scale) -> tuple[float, float]:
+    """Validate the query and options of a read over sources already known
+    to be valid BF16 ``[..., D]`` rows on ``device`` (a source bank's own
+    slots); the query checks and messages are those of ``check_sources``."""
+    if not isinstance(query, torch.Tensor):
+        raise TypeError("query must be a tensor")
+    if query.ndim != 1:
+        raise ValueError("query must have 1 dimensions")
+    if query.dtype != torch.bfloat16:
+        raise TypeError("query must use BF16 storage")
+    if query.device != device:
+        raise TypeError("query must be on the values device")
+    if not 1 <= int(query.shape[0]) <= width:
+        raise ValueError("query rank must satisfy 1<=R<=D")
+    return check_scalar(eps, "eps", positive=True), check_scalar(scale, "scale")
+
+
+__all__ = ["check_packed", "check_query", "check_scalar", "check_sources"]

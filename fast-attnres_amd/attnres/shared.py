@@ -26,6 +26,11 @@ fresh sum, also after a pass that stopped short of the sources (e.g.
 (the bank holds state between the reads' backward calls); first-order
 gradients, like the read itself.
 
+The autograd nodes hold the buffers and the per-pass bookkeeping in a state
+object that holds no token, so the buffers are freed with the graph, without
+waiting for Python's cycle collector (a node that held the bank itself would
+close a cycle bank -> token -> node -> bank).
+
 The reference has no counterpart: its shared sources' gradients are summed
 by autograd (the Block-schedule reads of `benchmarks/model.py:306-338`).
 """
@@ -40,7 +45,7 @@ from torch import Tensor
 
 from . import _native
 from ._ops import _contiguous, _dq_workspace, _source_table, _stream, packed_forward_impl, sources_forward_impl
-from ._sources import _EPS, _MAX_SOURCES, _MAX_WIDTH, check_packed, check_sources
+from ._sources import _EPS, _MAX_SOURCES, _MAX_WIDTH, check_query, check_sources
 
 _DTYPE_F32, _DTYPE_BF16 = 0, 1  # attnres_hip.h ATTNRES_DTYPE_*
 
@@ -57,34 +62,14 @@ def _pass_id() -> int:
     return torch._C._current_graph_task_id()
 
 
-class SharedSources:
-    """An ordered list of BF16 sources read by several queries (see module doc)."""
+class _SharedState:
+    """The sources and this pass's gradient sums, used by the nodes of a
+    ``SharedSources``."""
 
-    def __init__(self, sources: Sequence[Tensor]) -> None:
-        if not isinstance(sources, (list, tuple)) or not sources:
-            raise TypeError("sources must be a non-empty list or tuple of tensors")
-        first = sources[0]
-        if not isinstance(first, Tensor):
-            raise TypeError("values must contain only tensors")
-        probe = torch.empty(1, device=first.device, dtype=torch.bfloat16)
-        checked, _, _ = check_sources(tuple(sources), probe, _EPS, 1.0)
-        if not checked[0].is_cuda:
-            raise RuntimeError("attnres requires CUDA (ROCm/HIP) device tensors")
-        self.sources = checked
+    def __init__(self, sources: tuple[Tensor, ...]) -> None:
+        self.sources = sources
         self._grads: list[Tensor] | None = None
         self._pass = -1
-        self._token = _Gather.apply(self, *checked)
-
-    def __len__(self) -> int:
-        return len(self.sources)
-
-    def read(self, query: Tensor, *, eps: float = _EPS, scale: float = 1.0) -> Tensor:
-        """``attnres(sources, query, eps=eps, scale=scale)`` with the source
-        gradients summed in the kernels across this bank's reads."""
-        _, eps_value, scale_value = check_sources(self.sources, query, eps, scale)
-        return _Read.apply(self, self._token, query, eps_value, scale_value)
-
-    # ------------------------------------------------------------ backward
 
     def _backward(self, query: Tensor, out: Tensor, out_refine: Tensor, grad_out: Tensor,
                   logit: Tensor, inv_rms: Tensor, stats: Tensor, scale: float) -> Tensor:
@@ -123,12 +108,42 @@ class SharedSources:
         return grads if self._pass == _pass_id() else None
 
 
+class SharedSources:
+    """An ordered list of BF16 sources read by several queries (see module doc)."""
+
+    def __init__(self, sources: Sequence[Tensor]) -> None:
+        if not isinstance(sources, (list, tuple)) or not sources:
+            raise TypeError("sources must be a non-empty list or tuple of tensors")
+        first = sources[0]
+        if not isinstance(first, Tensor):
+            raise TypeError("values must contain only tensors")
+        probe = torch.empty(1, device=first.device, dtype=torch.bfloat16)
+        checked, _, _ = check_sources(tuple(sources), probe, _EPS, 1.0)
+        if not checked[0].is_cuda:
+            raise RuntimeError("attnres requires CUDA (ROCm/HIP) device tensors")
+        self._state = _SharedState(checked)
+        self._token = _Gather.apply(self._state, *checked)
+
+    @property
+    def sources(self) -> tuple[Tensor, ...]:
+        return self._state.sources
+
+    def __len__(self) -> int:
+        return len(self.sources)
+
+    def read(self, query: Tensor, *, eps: float = _EPS, scale: float = 1.0) -> Tensor:
+        """``attnres(sources, query, eps=eps, scale=scale)`` with the source
+        gradients summed in the kernels across this bank's reads."""
+        _, eps_value, scale_value = check_sources(self.sources, query, eps, scale)
+        return _Read.apply(self._state, self._token, query, eps_value, scale_value)
+
+
 class _Gather(torch.autograd.Function):
     """The bank's autograd node: its backward hands the summed gradients to
     the sources after every read's backward."""
 
     @staticmethod
-    def forward(ctx, bank: SharedSources, *sources: Tensor) -> Tensor:
+    def forward(ctx, bank: _SharedState, *sources: Tensor) -> Tensor:
         ctx.bank = bank
         return sources[0].new_empty((0,))
 
@@ -143,7 +158,7 @@ class _Gather(torch.autograd.Function):
 
 class _Read(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, bank: SharedSources, token: Tensor, query: Tensor, eps: float, scale: float) -> Tensor:
+    def forward(ctx, bank: _SharedState, token: Tensor, query: Tensor, eps: float, scale: float) -> Tensor:
         query = _contiguous(query)
         # always saved: the accumulating kernels read the refinement
         out, out_refine, logit, inv_rms, stats = sources_forward_impl(list(bank.sources), query, eps, scale, True)
@@ -161,134 +176,18 @@ class _Read(torch.autograd.Function):
         return None, token_grad, grad_query if ctx.needs_input_grad[2] else None, None, None
 
 
-class SourceBank:
-    """Sources kept in numbered slots of one packed BF16 buffer and read as
-    slot lists: the residual stream of a Full- or Block-schedule model.
+class _BankState:
+    """The slot buffer and this pass's gradient bookkeeping, used by the
+    nodes of a ``SourceBank``."""
 
-    Full schedule (read i sees every source pushed before it)::
-
-        bank = SourceBank(capacity=2 * layers + 1)
-        bank.push(embedding)                      # slot 0; any float dtype, shape [..., D]
-        x = bank.read(query_0)                    # attnres over slot 0 (BF16 out)
-        bank.push(sublayer(x.to(dtype)))          # slot 1
-        x = bank.read(query_1)                    # over slots 0..1, ...
-
-    Block schedule (a read sees the completed blocks, slots 0..k-1, plus the
-    running partial sum of the current block in some other slot)::
-
-        bank.push(embedding, slot=0)
-        bank.push(first_emitted, slot=p)          # the partial starts as one output
-        x = bank.read(query, count=1, tail=p)     # attnres(embedding, partial)
-        partial = bank.push_sum(partial, emitted, slot=q)   # partial + emitted, one pass
-
-    Each source is converted to BF16 once, into its slot, so a read passes
-    slot rows (the prefix view ``buffer[:count]``, or a list of slot pointers
-    when a tail slot is added) with no per-read conversion or stack.
-    ``push_sum`` adds the block's partial and the new output and writes the
-    sum (in their dtype, returned) and its BF16 copy (into the slot) in one
-    kernel (``attnres_hip_partial_sum``).
-
-    Gradients (``gradients="gather"``, the default): a read's backward writes
-    no dv rows, only its dq and the per-token coefficients of its dv
-    (``attnres_hip_{packed,sources}_backward_coef``), and keeps its BF16 dO.
-    Slot i's gradient is formed once, when the slot's push node runs its
-    backward -- after every read that saw slot i, since those reads take the
-    node's token as an input -- by ``attnres_hip_bank_gather``: one FP32 pass
-    over the dO rows of those reads.  ``gradients="accumulate"`` instead adds
-    every read's FP32 dv into one FP32 ``[capacity, ..., D]`` buffer in the
-    backward kernel (``attnres_hip_{packed,sources}_backward_accumulate_f32``:
-    a read-modify-write of the sum per read).  Either way the sums are FP32
-    without BF16 rounding of the per-read dv, and reach the source in its
-    dtype.  Eager mode only; one bank per forward pass.
-    """
-
-    def __init__(self, capacity: int, *, gradients: str = "gather") -> None:
-        if isinstance(capacity, bool) or not isinstance(capacity, int) or not 1 <= capacity <= _MAX_SOURCES:
-            raise ValueError(f"capacity must be an integer in 1..{_MAX_SOURCES}")
-        if gradients not in ("gather", "accumulate"):
-            raise ValueError("gradients must be 'gather' or 'accumulate'")
+    def __init__(self, capacity: int, gradients: str) -> None:
         self.capacity = capacity
         self.gradients = gradients
-        self._pending: list[list[tuple[tuple, int]]] = [[] for _ in range(capacity)]
         self._values: Tensor | None = None
-        self._tokens: list[Tensor | None] = [None] * capacity
         self._grads: Tensor | None = None
         self._written: list[bool] = [False] * capacity
+        self._pending: list[list[tuple[tuple, int]]] = [[] for _ in range(capacity)]
         self._pass = -1
-
-    def __len__(self) -> int:
-        """Number of pushed slots."""
-        return sum(token is not None for token in self._tokens)
-
-    def _claim(self, source: Tensor, slot: int | None) -> int:
-        if not isinstance(source, Tensor) or not source.is_floating_point():
-            raise TypeError("a source must be a floating-point tensor")
-        if not source.is_cuda:
-            raise RuntimeError("attnres requires CUDA (ROCm/HIP) device tensors")
-        if slot is None:
-            free = [i for i, token in enumerate(self._tokens) if token is None]
-            if not free:
-                raise ValueError("the source bank is full")
-            slot = free[0]
-        if isinstance(slot, bool) or not isinstance(slot, int) or not 0 <= slot < self.capacity:
-            raise ValueError(f"slot must be an integer in 0..{self.capacity - 1}")
-        if self._tokens[slot] is not None:
-            raise ValueError(f"slot {slot} already holds a source")
-        if self._values is None:
-            if source.ndim < 1 or source.numel() == 0 or not 1 <= source.shape[-1] <= _MAX_WIDTH:
-                raise ValueError("each source must have shape [...,D]")
-            self._values = torch.empty((self.capacity, *source.shape), device=source.device, dtype=torch.bfloat16)
-        elif source.shape != self._values.shape[1:] or source.device != self._values.device:
-            raise ValueError("all source tensors must have the same logical shape and device")
-        return slot
-
-    def push(self, source: Tensor, *, slot: int | None = None) -> int:
-        """Store ``source`` (``[..., D]``, any float dtype, on the GPU) in
-        ``slot`` (default: the lowest free one); returns the slot."""
-        slot = self._claim(source, slot)
-        self._tokens[slot] = _Push.apply(self, slot, source)
-        return slot
-
-    def push_sum(self, prev: Tensor, emitted: Tensor, *, slot: int | None = None) -> Tensor:
-        """``prev + emitted`` (FP32 or BF16, same shape and dtype), returned in
-        that dtype and stored as BF16 in ``slot`` -- one kernel for the
-        Block schedule's partial sum and its BF16 copy."""
-        if not isinstance(prev, Tensor) or not isinstance(emitted, Tensor):
-            raise TypeError("push_sum takes two tensors")
-        if prev.shape != emitted.shape or prev.dtype != emitted.dtype or prev.device != emitted.device:
-            raise ValueError("push_sum needs tensors of one shape, dtype and device")
-        if prev.dtype not in (torch.float32, torch.bfloat16):
-            raise TypeError("push_sum supports float32 and bfloat16 tensors")
-        slot = self._claim(emitted, slot)
-        partial, token = _PushSum.apply(self, slot, prev, emitted)
-        self._tokens[slot] = token
-        return partial
-
-    def read(self, query: Tensor, *, count: int | None = None, tail: int | None = None, eps: float = _EPS,
-             scale: float = 1.0) -> Tensor:
-        """``attnres`` over slots ``0..count-1`` (default: every pushed slot,
-        which must then be ``0..len-1``) followed by slot ``tail`` if given; BF16."""
-        if count is None:
-            if tail is not None:
-                raise ValueError("a read with a tail slot needs count")
-            count = len(self)
-        if isinstance(count, bool) or not isinstance(count, int) or not 0 <= count <= self.capacity:
-            raise ValueError("count must be a number of leading slots")
-        if any(self._tokens[i] is None for i in range(count)):
-            raise ValueError("count must select pushed slots 0..count-1")
-        slots = list(range(count))
-        if tail is not None:
-            if isinstance(tail, bool) or not isinstance(tail, int) or not count <= tail < self.capacity \
-                    or self._tokens[tail] is None:
-                raise ValueError("tail must be a pushed slot after the leading ones")
-            slots.append(tail)
-        if not slots:
-            raise ValueError("a read needs at least one source")
-        if tail is None:
-            eps_value, scale_value = check_packed(self._values[:count], query, eps, scale)
-        else:
-            _, eps_value, scale_value = check_sources(tuple(self._values[i] for i in slots), query, eps, scale)
-        return _BankRead.apply(self, tuple(slots), query, eps_value, scale_value, *[self._tokens[i] for i in slots])
 
     def _sources(self, slots: tuple[int, ...]) -> list[Tensor]:
         return [self._values[i] for i in slots]
@@ -369,8 +268,11 @@ class SourceBank:
                     pointers, strides, count, tokens, width, query.data_ptr(), rank, scale, *saved, coef.data_ptr(),
                     grad_query.data_ptr(), workspace.data_ptr(), workspace.numel(), _stream(device))
         _native.check(status, "attnres source-bank coefficient backward")
-        query_row = torch.zeros((width,), device=device, dtype=torch.bfloat16)
-        query_row[width - rank:] = query.reshape(-1)
+        if rank == width:
+            query_row = query
+        else:  # the query is aligned to the row's last R elements, zeros before
+            query_row = torch.zeros((width,), device=device, dtype=torch.bfloat16)
+            query_row[width - rank:] = query.reshape(-1)
         record = (grad_out, query_row, coef, count, rank)
         for position, slot in enumerate(slots):
             self._pending[slot].append((record, position))
@@ -404,17 +306,156 @@ class SourceBank:
         return grad
 
 
+class SourceBank:
+    """Sources kept in numbered slots of one packed BF16 buffer and read as
+    slot lists: the residual stream of a Full- or Block-schedule model.
+
+    Full schedule (read i sees every source pushed before it)::
+
+        bank = SourceBank(capacity=2 * layers + 1)
+        bank.push(embedding)                      # slot 0; any float dtype, shape [..., D]
+        x = bank.read(query_0)                    # attnres over slot 0 (BF16 out)
+        bank.push(sublayer(x.to(dtype)))          # slot 1
+        x = bank.read(query_1)                    # over slots 0..1, ...
+
+    Block schedule (a read sees the completed blocks, slots 0..k-1, plus the
+    running partial sum of the current block in some other slot)::
+
+        bank.push(embedding, slot=0)
+        bank.push(first_emitted, slot=p)          # the partial starts as one output
+        x = bank.read(query, count=1, tail=p)     # attnres(embedding, partial)
+        partial = bank.push_sum(partial, emitted, slot=q)   # partial + emitted, one pass
+
+    Each source is converted to BF16 once, into its slot, so a read passes
+    slot rows (the prefix view ``buffer[:count]``, or a list of slot pointers
+    when a tail slot is added) with no per-read conversion or stack.
+    ``push_sum`` adds the block's partial and the new output and writes the
+    sum (in their dtype, returned) and its BF16 copy (into the slot) in one
+    kernel (``attnres_hip_partial_sum``).
+
+    Gradients (``gradients="gather"``, the default): a read's backward writes
+    no dv rows, only its dq and the per-token coefficients of its dv
+    (``attnres_hip_{packed,sources}_backward_coef``), and keeps its BF16 dO.
+    Slot i's gradient is formed once, when the slot's push node runs its
+    backward, by ``attnres_hip_bank_gather``: one FP32 pass over the dO rows
+    of the reads that saw slot i.  The ordering uses one chain of zero-size
+    tokens: every push node takes the token of the push before it, and a
+    read takes the latest token, so a push node's backward runs after that
+    of every read made after the push (those that saw the slot among them),
+    and a read has one token input however many slots it reads.  ``gradients="accumulate"`` instead adds
+    every read's FP32 dv into one FP32 ``[capacity, ..., D]`` buffer in the
+    backward kernel (``attnres_hip_{packed,sources}_backward_accumulate_f32``:
+    a read-modify-write of the sum per read).  Either way the sums are FP32
+    without BF16 rounding of the per-read dv, and reach the source in its
+    dtype.  Eager mode only; one bank per forward pass.
+    """
+
+    def __init__(self, capacity: int, *, gradients: str = "gather") -> None:
+        if isinstance(capacity, bool) or not isinstance(capacity, int) or not 1 <= capacity <= _MAX_SOURCES:
+            raise ValueError(f"capacity must be an integer in 1..{_MAX_SOURCES}")
+        if gradients not in ("gather", "accumulate"):
+            raise ValueError("gradients must be 'gather' or 'accumulate'")
+        self.capacity = capacity
+        self.gradients = gradients
+        self._state = _BankState(capacity, gradients)
+        self._pushed: list[bool] = [False] * capacity
+        self._token: Tensor | None = None  # the latest push's token
+
+    def __len__(self) -> int:
+        """Number of pushed slots."""
+        return sum(self._pushed)
+
+    def _claim(self, source: Tensor, slot: int | None) -> int:
+        if not isinstance(source, Tensor) or not source.is_floating_point():
+            raise TypeError("a source must be a floating-point tensor")
+        if not source.is_cuda:
+            raise RuntimeError("attnres requires CUDA (ROCm/HIP) device tensors")
+        if slot is None:
+            free = [i for i, pushed in enumerate(self._pushed) if not pushed]
+            if not free:
+                raise ValueError("the source bank is full")
+            slot = free[0]
+        if isinstance(slot, bool) or not isinstance(slot, int) or not 0 <= slot < self.capacity:
+            raise ValueError(f"slot must be an integer in 0..{self.capacity - 1}")
+        if self._pushed[slot]:
+            raise ValueError(f"slot {slot} already holds a source")
+        state = self._state
+        if state._values is None:
+            if source.ndim < 1 or source.numel() == 0 or not 1 <= source.shape[-1] <= _MAX_WIDTH:
+                raise ValueError("each source must have shape [...,D]")
+            state._values = torch.empty((self.capacity, *source.shape), device=source.device, dtype=torch.bfloat16)
+        elif source.shape != state._values.shape[1:] or source.device != state._values.device:
+            raise ValueError("all source tensors must have the same logical shape and device")
+        return slot
+
+    def push(self, source: Tensor, *, slot: int | None = None) -> int:
+        """Store ``source`` (``[..., D]``, any float dtype, on the GPU) in
+        ``slot`` (default: the lowest free one); returns the slot."""
+        slot = self._claim(source, slot)
+        self._token = _Push.apply(self._state, slot, source, self._token)
+        self._pushed[slot] = True
+        return slot
+
+    def push_sum(self, prev: Tensor, emitted: Tensor, *, slot: int | None = None) -> Tensor:
+        """``prev + emitted`` (FP32 or BF16, same shape and dtype), returned in
+        that dtype and stored as BF16 in ``slot`` -- one kernel for the
+        Block schedule's partial sum and its BF16 copy."""
+        if not isinstance(prev, Tensor) or not isinstance(emitted, Tensor):
+            raise TypeError("push_sum takes two tensors")
+        if prev.shape != emitted.shape or prev.dtype != emitted.dtype or prev.device != emitted.device:
+            raise ValueError("push_sum needs tensors of one shape, dtype and device")
+        if prev.dtype not in (torch.float32, torch.bfloat16):
+            raise TypeError("push_sum supports float32 and bfloat16 tensors")
+        slot = self._claim(emitted, slot)
+        partial, self._token = _PushSum.apply(self._state, slot, prev, emitted, self._token)
+        self._pushed[slot] = True
+        return partial
+
+    def read(self, query: Tensor, *, count: int | None = None, tail: int | None = None, eps: float = _EPS,
+             scale: float = 1.0) -> Tensor:
+        """``attnres`` over slots ``0..count-1`` (default: every pushed slot,
+        which must then be ``0..len-1``) followed by slot ``tail`` if given; BF16."""
+        if count is None:
+            if tail is not None:
+                raise ValueError("a read with a tail slot needs count")
+            count = len(self)
+        if isinstance(count, bool) or not isinstance(count, int) or not 0 <= count <= self.capacity:
+            raise ValueError("count must be a number of leading slots")
+        if not all(self._pushed[:count]):
+            raise ValueError("count must select pushed slots 0..count-1")
+        slots = list(range(count))
+        if tail is not None:
+            if isinstance(tail, bool) or not isinstance(tail, int) or not count <= tail < self.capacity \
+                    or not self._pushed[tail]:
+                raise ValueError("tail must be a pushed slot after the leading ones")
+            slots.append(tail)
+        if not slots:
+            raise ValueError("a read needs at least one source")
+        # the slots were checked at their push: BF16 rows [..., D] on one device
+        values = self._state._values
+        eps_value, scale_value = check_query(query, int(values.shape[-1]), values.device, eps, scale)
+        return _BankRead.apply(self._state, tuple(slots), query, eps_value, scale_value, self._token)
+
+
+def _token_input_grad(ctx, index: int) -> Tensor | None:
+    """The zero-size gradient of a token input (None when it has none)."""
+    return torch.empty((0,), device=ctx.token_device) if ctx.needs_input_grad[index] else None
+
+
 class _Push(torch.autograd.Function):
+    """Copy a source into its slot; the new token follows ``previous`` (the
+    token of the push before, None for the first)."""
+
     @staticmethod
-    def forward(ctx, bank: SourceBank, slot: int, source: Tensor) -> Tensor:
+    def forward(ctx, bank: _BankState, slot: int, source: Tensor, previous: Tensor | None) -> Tensor:
         bank._values[slot].copy_(source.detach())
-        ctx.bank, ctx.slot, ctx.dtype = bank, slot, source.dtype
+        ctx.bank, ctx.slot, ctx.dtype, ctx.token_device = bank, slot, source.dtype, source.device
         return source.new_empty((0,))
 
     @staticmethod
     def backward(ctx, _token_grad):
         grad = ctx.bank._take(ctx.slot)
-        return None, None, None if grad is None else grad.to(ctx.dtype)
+        return None, None, None if grad is None else grad.to(ctx.dtype), _token_input_grad(ctx, 3)
 
 
 class _PushSum(torch.autograd.Function):
@@ -423,7 +464,7 @@ class _PushSum(torch.autograd.Function):
     the slot's summed read gradient."""
 
     @staticmethod
-    def forward(ctx, bank: SourceBank, slot: int, prev: Tensor, emitted: Tensor):
+    def forward(ctx, bank: _BankState, slot: int, prev: Tensor, emitted: Tensor, previous: Tensor | None):
         lib = _native.load()
         prev, emitted = _contiguous(prev.detach()), _contiguous(emitted.detach())
         partial = torch.empty_like(emitted)
@@ -433,7 +474,7 @@ class _PushSum(torch.autograd.Function):
                                                  partial.data_ptr(), bank._values[slot].data_ptr(),
                                                  _stream(emitted.device))
         _native.check(status, "attnres partial sum")
-        ctx.bank, ctx.slot, ctx.dtype = bank, slot, emitted.dtype
+        ctx.bank, ctx.slot, ctx.dtype, ctx.token_device = bank, slot, emitted.dtype, emitted.device
         return partial, emitted.new_empty((0,))
 
     @staticmethod
@@ -443,13 +484,13 @@ class _PushSum(torch.autograd.Function):
             grad = grad.to(ctx.dtype) if grad_partial is None else grad_partial + grad.to(ctx.dtype)
         else:
             grad = grad_partial
-        return None, None, grad, grad
+        return None, None, grad, grad, _token_input_grad(ctx, 4)
 
 
 class _BankRead(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, bank: SourceBank, slots: tuple[int, ...], query: Tensor, eps: float, scale: float,
-                *tokens: Tensor) -> Tensor:
+    def forward(ctx, bank: _BankState, slots: tuple[int, ...], query: Tensor, eps: float, scale: float,
+                token: Tensor) -> Tensor:
         query = _contiguous(query)
         shape = bank._values.shape[1:]
         if bank._prefix(slots):
@@ -460,7 +501,7 @@ class _BankRead(torch.autograd.Function):
                                                                          True)
         # always saved: the accumulating kernels read the refinement
         ctx.bank, ctx.slots, ctx.scale = bank, slots, scale
-        ctx.token_device = tokens[0].device
+        ctx.token_device = token.device
         ctx.save_for_backward(query, out, out_refine, logit, inv_rms, stats)
         return out.reshape(shape)
 
@@ -469,9 +510,7 @@ class _BankRead(torch.autograd.Function):
         query, out, out_refine, logit, inv_rms, stats = ctx.saved_tensors
         grad_query = ctx.bank._backward(ctx.slots, query, out, out_refine, grad_out, logit, inv_rms, stats,
                                         ctx.scale)
-        empty = torch.empty((0,), device=ctx.token_device)
-        return (None, None, grad_query if ctx.needs_input_grad[2] else None, None, None,
-                *([empty] * len(ctx.slots)))
+        return None, None, grad_query if ctx.needs_input_grad[2] else None, None, None, _token_input_grad(ctx, 5)
 
 
 __all__ = ["SharedSources", "SourceBank"]

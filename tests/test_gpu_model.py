@@ -186,6 +186,9 @@ def test_bf16_autocast_model_with_and_without_the_bank(mode):
         assert _relative_error(q.grad, p.grad) < 3e-2, name
     optimizer = torch.optim.AdamW(banked.parameters(), lr=3e-3)
     targets = torch.roll(tokens, -1, dims=1)
-    with torch.autocast("cuda", dtype=torch.bfloat16):
-        losses = [float(training_step(banked, optimizer, tokens, targets)) for _ in range(8)]
+    losses = []
+    for _ in range(8):
+        # one autocast context per step: a context kept across steps reuses its BF16 weight casts
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            losses.append(float(training_step(banked, optimizer, tokens, targets)))
     assert losses[-1] < losses[0]

@@ -97,7 +97,7 @@ def test_random_source_bank_stream_matches_attnres(index):
             slot = completed + r
             if bank_mode:
                 partial = emitted[r] if partial is None else bank.push_sum(partial, emitted[r], slot=slot)
-                if bank._tokens[slot] is None:
+                if not bank._pushed[slot]:
                     bank.push(partial, slot=slot)
                 out = bank.read(queries[r], count=count, tail=slot if with_partial else None)
             else:

@@ -12,6 +12,7 @@ token count (9 separately allocated sources, 3 reads) plus a masked width.
 
 from __future__ import annotations
 
+import gc
 import math
 
 import pytest
@@ -196,7 +197,7 @@ def test_push_sum_is_the_add_and_the_cast(shape, dtype):
     partial = bank.push_sum(prev, emitted, slot=1)
     expected = prev + emitted
     assert partial.dtype == dtype and torch.equal(partial, expected)
-    assert torch.equal(bank._values[1], expected.to(torch.bfloat16))
+    assert torch.equal(bank._state._values[1], expected.to(torch.bfloat16))
     grad = torch.randn_like(partial)
     gp, ge = torch.autograd.grad(partial, (prev, emitted), grad)
     assert torch.equal(gp, grad) and torch.equal(ge, grad)
@@ -331,3 +332,33 @@ def test_source_bank_source_also_used_outside_the_bank():
         rx, ry = torch.autograd.grad((ref.float() * 3).sum() + (x * x).sum(), (x, y))
         torch.testing.assert_close(gx, rx, rtol=2.0**-6, atol=2.0**-6 * float(rx.abs().max()))
         torch.testing.assert_close(gy, ry, rtol=2.0**-6, atol=2.0**-6 * float(ry.abs().max()))
+
+
+def test_banks_free_their_buffers_with_the_graph():
+    """The buffers of a SourceBank (slots, sums, kept dO rows) and of a
+    SharedSources (sums) are freed as soon as the graph and the outputs are
+    gone, with Python's cycle collector off: nothing forms a reference cycle
+    through the bank object."""
+    from attnres import SourceBank
+
+    embedded, weights, queries, grads = _stream_case(512, 512)
+    src, shared_queries, shared_grads, _ = _case(sources=4, tokens=(64,), width=512, rank=512, reads=2)
+    gc.collect()
+    torch.cuda.synchronize()
+    gc.disable()
+    try:
+        before = torch.cuda.memory_allocated()
+        for gradients in ("gather", "accumulate"):
+            bank = SourceBank(len(weights) + 1, gradients=gradients)
+            outs = _run_stream(lambda q: bank.read(q.to(torch.bfloat16)).float(), bank.push, embedded, weights,
+                               queries)
+            result = torch.autograd.grad(outs, (embedded, *queries), grads)
+            del bank, outs, result
+            assert torch.cuda.memory_allocated() == before, gradients
+        shared = SharedSources(src)
+        outs = [shared.read(q) for q in shared_queries]
+        result = torch.autograd.grad(outs, src, shared_grads)
+        del shared, outs, result
+        assert torch.cuda.memory_allocated() == before
+    finally:
+        gc.enable()
