@@ -39,7 +39,14 @@ and the line reports the summed operator time per step.
 ``model`` is the caller: one training step (forward, backward, AdamW) of the
 24-layer Full-schedule causal LM of ``benchmarks/model.py`` at D=1024 on
 16x1024 tokens, whose 48 residual reads (S = 2..49) are the HIP operator; the
-rest of the model runs in FP32 PyTorch.
+rest of the model runs in FP32 PyTorch (``--autocast bf16``: under BF16
+autocast, entered once per step).  ``model_block`` is the same model on the
+Block schedule; ``model_ref`` is the reference's own 24-layer workload
+(batch 2 x 1024 tokens, vocab 32768, BF16 autocast, fused AdamW).
+
+The c2..c3 lines also carry ``graph_replay``: the forward, the backward and
+the whole read through the C ABI captured into HIP graphs and replayed (the
+kernels' time without host or launch gaps), median and quartiles over rounds.
 
 ``--copy-probe`` runs only a plain device copy of known size, used to scale
 the hardware FETCH_SIZE / WRITE_SIZE counters when profiling.
@@ -177,11 +184,13 @@ def cpu_baseline(values, query, grad_out, budget_s: float, chunk: int) -> dict:
     }
 
 
-def graph_replay(values, query, grad_out, cfg: dict, replays: int, rounds: int = 5) -> dict:
-    """fwd+bwd of one packed read through the C ABI, captured into a HIP graph
-    and replayed: the reference harness's "cuda_graph" boundary (an event
-    interval around fixed graph replays, benchmarks/run.py:590-599), i.e. the
-    kernels' time without host or launch gaps.  Best of `rounds`."""
+def graph_replay(values, query, grad_out, cfg: dict, replays: int = 20, rounds: int = 11) -> dict:
+    """The read through the C ABI, captured into HIP graphs and replayed: the
+    reference harness's "cuda_graph" boundary (an event interval around fixed
+    graph replays, benchmarks/run.py:590-599), i.e. the kernels' time without
+    host or launch gaps.  Three graphs (forward, backward, forward + backward),
+    each replayed ``replays`` times per round over ``rounds`` rounds after one
+    warm-up round; per graph the median, quartiles and best round."""
     import ctypes
     import re
 
@@ -213,47 +222,56 @@ def graph_replay(values, query, grad_out, cfg: dict, replays: int, rounds: int =
     refine_ptr = refine.data_ptr() if refine.numel() else None
     stream = torch.cuda.Stream()
 
-    def enqueue():
-        h = stream.cuda_stream
-        st = lib.attnres_hip_packed_forward(packed.data_ptr(), N * width, width, S, N, width, query.data_ptr(), rank,
-                                            2.0**-23, 1.0, out.data_ptr(), refine_ptr, logit.data_ptr(),
-                                            inv_rms.data_ptr(), stats.data_ptr(), h)
-        st = st or lib.attnres_hip_packed_backward(
+    def forward(h):
+        return lib.attnres_hip_packed_forward(packed.data_ptr(), N * width, width, S, N, width, query.data_ptr(),
+                                              rank, 2.0**-23, 1.0, out.data_ptr(), refine_ptr, logit.data_ptr(),
+                                              inv_rms.data_ptr(), stats.data_ptr(), h)
+
+    def backward(h):
+        return lib.attnres_hip_packed_backward(
             packed.data_ptr(), N * width, width, S, N, width, query.data_ptr(), rank, 1.0,
             out.data_ptr() if refine_ptr else None, refine_ptr, g.data_ptr(), logit.data_ptr(), inv_rms.data_ptr(),
             stats.data_ptr(), dv.data_ptr(), dq.data_ptr(), ws.data_ptr(), ws.numel(), h)
-        _native.check(st, "graph-replay read")
 
+    parts = {"forward": (forward,), "backward": (backward,), "read": (forward, backward)}
+    fwd_bytes, bwd_bytes = read_bytes(S, N, width)
+    part_bytes = {"forward": fwd_bytes, "backward": bwd_bytes, "read": fwd_bytes + bwd_bytes}
     stream.wait_stream(torch.cuda.current_stream())
-    enqueue()  # eager first: the library's per-thread launch caches are filled outside capture
+    for call in (forward, backward):  # eager first: the library's per-thread launch caches fill outside capture
+        _native.check(call(stream.cuda_stream), "graph-replay read")
     torch.cuda.synchronize()
-    graph, exe = vp(), vp()
-    assert hip.hipStreamBeginCapture(vp(stream.cuda_stream), 2) == 0  # relaxed
-    enqueue()
-    assert hip.hipStreamEndCapture(vp(stream.cuda_stream), ctypes.byref(graph)) == 0
-    assert hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0) == 0
-    try:
-        times = []
-        for round_index in range(rounds + 1):  # round 0 warms up
-            start, stop = _event(), _event()
-            with torch.cuda.stream(stream):
-                start.record()
-                for _ in range(replays):
-                    assert hip.hipGraphLaunch(exe, vp(stream.cuda_stream)) == 0
-                stop.record()
-            torch.cuda.synchronize()
-            if round_index:
-                times.append(start.elapsed_time(stop) / replays)
-        best = min(times)
-        fwd_bytes, bwd_bytes = read_bytes(S, N, width)
-        tbs = (fwd_bytes + bwd_bytes) / (best * 1e-3) / 1e12
-        return {"us_per_read": round(best * 1e3, 2), "TB/s": round(tbs, 4),
-                "pct_of_peak": round(100 * tbs / HBM_PEAK_TBS, 2), "replays": replays, "rounds": rounds,
-                "boundary": "HIP events around back-to-back replays of a graph holding the C-ABI forward and "
-                            "backward (reference harness cuda_graph boundary); best round"}
-    finally:
-        hip.hipGraphExecDestroy(exe)
-        hip.hipGraphDestroy(graph)
+    result = {}
+    for part, calls in parts.items():
+        graph, exe = vp(), vp()
+        assert hip.hipStreamBeginCapture(vp(stream.cuda_stream), 2) == 0  # relaxed
+        for call in calls:
+            _native.check(call(stream.cuda_stream), "graph-replay read")
+        assert hip.hipStreamEndCapture(vp(stream.cuda_stream), ctypes.byref(graph)) == 0
+        assert hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0) == 0
+        try:
+            times = []
+            for round_index in range(rounds + 1):  # round 0 warms up
+                start, stop = _event(), _event()
+                with torch.cuda.stream(stream):
+                    start.record()
+                    for _ in range(replays):
+                        assert hip.hipGraphLaunch(exe, vp(stream.cuda_stream)) == 0
+                    stop.record()
+                torch.cuda.synchronize()
+                if round_index:
+                    times.append(start.elapsed_time(stop) / replays * 1e3)
+        finally:
+            hip.hipGraphExecDestroy(exe)
+            hip.hipGraphDestroy(graph)
+        q1, median, q3 = statistics.quantiles(times, n=4)
+        tbs = part_bytes[part] / (median * 1e-6) / 1e12
+        result[part] = {"us_median": round(median, 2), "us_q1": round(q1, 2), "us_q3": round(q3, 2),
+                        "us_best": round(min(times), 2), "TB/s": round(tbs, 4),
+                        "pct_of_peak": round(100 * tbs / HBM_PEAK_TBS, 2)}
+    result["replays"], result["rounds"] = replays, rounds
+    result["boundary"] = ("HIP events around back-to-back replays of graphs holding the C-ABI forward, backward, and "
+                          "forward + backward (reference harness cuda_graph boundary); TB/s from the median round")
+    return result
 
 
 def _event():
@@ -741,7 +759,7 @@ def main(argv=None) -> int:
         "cpu_baseline": None,
     }
     # the same read through the C ABI, captured into a HIP graph and replayed
-    record["graph_replay"] = graph_replay(values, query, grad_out, cfg, replays=max(args.steps // 5, 4))
+    record["graph_replay"] = graph_replay(values, query, grad_out, cfg)
     if not args.no_cpu_baseline:
         record["cpu_baseline"] = cpu_baseline(values.detach(), query.detach(), grad_out,
                                               args.cpu_budget, chunk=2048)
