@@ -35,6 +35,7 @@ forward and read in the backward instead of one.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import math
 from typing import Any
@@ -112,7 +113,16 @@ def _contiguous(tensor: Tensor) -> Tensor:
 
 
 def _stream(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The current stream's handle on ``device`` (no Python Stream object)."""
+    return torch._C._cuda_getCurrentRawStream(device.index)
+
+
+_NO_SWITCH = contextlib.nullcontext()
+
+
+def _on_device(device: torch.device):
+    """``torch.cuda.device(device)``, or nothing when it is the current device."""
+    return _NO_SWITCH if device.index == torch.cuda.current_device() else torch.cuda.device(device)
 
 
 def _rows_of(shape) -> int:
@@ -126,12 +136,27 @@ def _dq_workspace(lib, n_tokens: int, width: int, rank: int, device) -> Tensor:
     return torch.empty((elems,), device=device, dtype=_F32)
 
 
+def _statistics(tokens: int, sources: int, device, pooled: bool) -> tuple[Tensor, Tensor, Tensor]:
+    """logit ``[N, S]``, inv_rms ``[N, S]`` and stats ``[2, N]`` (FP32).
+    ``pooled``: views of one allocation, for callers that keep them together
+    (not for custom-op outputs, which must not alias each other)."""
+    if not pooled:
+        return (torch.empty((tokens, sources), device=device, dtype=_F32),
+                torch.empty((tokens, sources), device=device, dtype=_F32),
+                torch.empty((2, tokens), device=device, dtype=_F32))
+    block = tokens * sources
+    pool = torch.empty((2 * block + 2 * tokens,), device=device, dtype=_F32)
+    return (pool[:block].view(tokens, sources), pool[block:2 * block].view(tokens, sources),
+            pool[2 * block:].view(2, tokens))
+
+
 # ------------------------------------------------------------------ packed
 
 def packed_forward_impl(values: Tensor, query: Tensor, eps: float, scale: float,
-                        save: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+                        save: bool, pooled: bool = False) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """The packed forward launch; ``save`` chooses whether the refinement is
-    stored (``out_refine`` ``[N, D]``) or not (``[0, D]``)."""
+    stored (``out_refine`` ``[N, D]``) or not (``[0, D]``); ``pooled`` as for
+    ``_statistics``."""
     lib = _native.load()
     values = _unit_feature_stride(values)
     query = _contiguous(query)
@@ -139,10 +164,8 @@ def packed_forward_impl(values: Tensor, query: Tensor, eps: float, scale: float,
     device = values.device
     out = torch.empty((tokens, width), device=device, dtype=_BF16)
     out_refine = torch.empty((tokens if save else 0, width), device=device, dtype=torch.int8)
-    logit = torch.empty((tokens, sources), device=device, dtype=_F32)
-    inv_rms = torch.empty((tokens, sources), device=device, dtype=_F32)
-    stats = torch.empty((2, tokens), device=device, dtype=_F32)
-    with torch.cuda.device(device):
+    logit, inv_rms, stats = _statistics(tokens, sources, device, pooled)
+    with _on_device(device):
         status = lib.attnres_hip_packed_forward(
             values.data_ptr(), values.stride(0), values.stride(1), sources, tokens, width,
             query.data_ptr(), query.numel(), eps, scale, out.data_ptr(), _pointer(out_refine),
@@ -185,7 +208,7 @@ def packed_backward(values: Tensor, query: Tensor, out: Tensor, out_refine: Tens
     grad_values = torch.empty((sources, tokens, width), device=device, dtype=_BF16)
     grad_query = torch.empty((rank,), device=device, dtype=_BF16)
     workspace = _dq_workspace(lib, tokens, width, rank, device)
-    with torch.cuda.device(device):
+    with _on_device(device):
         status = lib.attnres_hip_packed_backward(
             values.data_ptr(), values.stride(0), values.stride(1), sources, tokens, width,
             query.data_ptr(), rank, scale, None if recompute else out.data_ptr(),
@@ -256,8 +279,9 @@ def _source_table(sources: list[Tensor]) -> tuple[list[Tensor], Any, Any]:
 
 
 def sources_forward_impl(sources: list[Tensor], query: Tensor, eps: float, scale: float,
-                         save: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
-    """The source-list forward launch; ``save`` as for ``packed_forward_impl``."""
+                         save: bool, pooled: bool = False) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """The source-list forward launch; ``save`` and ``pooled`` as for
+    ``packed_forward_impl``."""
     lib = _native.load()
     first = sources[0]
     query = _contiguous(query)
@@ -266,10 +290,8 @@ def sources_forward_impl(sources: list[Tensor], query: Tensor, eps: float, scale
     prepared, pointers, row_strides = _source_table(sources)
     out = torch.empty(first.shape, device=device, dtype=_BF16)
     out_refine = torch.empty((tokens if save else 0, width), device=device, dtype=torch.int8)
-    logit = torch.empty((tokens, count), device=device, dtype=_F32)
-    inv_rms = torch.empty((tokens, count), device=device, dtype=_F32)
-    stats = torch.empty((2, tokens), device=device, dtype=_F32)
-    with torch.cuda.device(device):
+    logit, inv_rms, stats = _statistics(tokens, count, device, pooled)
+    with _on_device(device):
         status = lib.attnres_hip_sources_forward(
             pointers, row_strides, count, tokens, width, query.data_ptr(), query.numel(),
             eps, scale, out.data_ptr(), _pointer(out_refine), logit.data_ptr(),
@@ -316,7 +338,7 @@ def sources_backward(sources: list[Tensor], query: Tensor, out: Tensor, out_refi
     grad_pointers = (ctypes.c_void_p * count)(*[grad.data_ptr() for grad in grads])
     grad_query = torch.empty((rank,), device=device, dtype=_BF16)
     workspace = _dq_workspace(lib, tokens, width, rank, device)
-    with torch.cuda.device(device):
+    with _on_device(device):
         status = lib.attnres_hip_sources_backward(
             pointers, row_strides, count, tokens, width, query.data_ptr(), rank, scale,
             None if recompute else out.data_ptr(), None if recompute else _contiguous(out_refine).data_ptr(),

@@ -38,13 +38,15 @@ by autograd (the Block-schedule reads of `benchmarks/model.py:306-338`).
 from __future__ import annotations
 
 import ctypes
+from array import array
 from typing import Sequence
 
 import torch
 from torch import Tensor
 
 from . import _native
-from ._ops import _contiguous, _dq_workspace, _source_table, _stream, packed_forward_impl, sources_forward_impl
+from ._ops import (_contiguous, _dq_workspace, _on_device, _source_table, _stream, packed_forward_impl,
+                   sources_forward_impl)
 from ._sources import _EPS, _MAX_SOURCES, _MAX_WIDTH, check_query, check_sources
 
 _DTYPE_F32, _DTYPE_BF16 = 0, 1  # attnres_hip.h ATTNRES_DTYPE_*
@@ -55,6 +57,11 @@ class _GatherRead(ctypes.Structure):
 
     _fields_ = [("grad_out", ctypes.c_void_p), ("query_row", ctypes.c_void_p), ("coef", ctypes.c_void_p),
                 ("n_sources", ctypes.c_int64), ("position", ctypes.c_int64), ("rank", ctypes.c_int64)]
+
+
+# A gather's read table is passed as an int64 array of the same layout (six
+# 8-byte fields per read), filled without per-field ctypes attribute writes.
+assert ctypes.sizeof(_GatherRead) == 6 * 8 and _GatherRead.position.offset == 4 * 8
 
 
 def _pass_id() -> int:
@@ -92,7 +99,7 @@ class _SharedState:
         grad_query = torch.empty((rank,), device=device, dtype=torch.bfloat16)
         workspace = _dq_workspace(lib, tokens, width, rank, device)
         grad_out = _contiguous(grad_out.to(torch.bfloat16))
-        with torch.cuda.device(device):
+        with _on_device(device):
             status = lib.attnres_hip_sources_backward_accumulate(
                 pointers, row_strides, count, tokens, width, query.data_ptr(), rank, scale,
                 _contiguous(out).data_ptr(), _contiguous(out_refine).data_ptr(), grad_out.data_ptr(),
@@ -161,7 +168,8 @@ class _Read(torch.autograd.Function):
     def forward(ctx, bank: _SharedState, token: Tensor, query: Tensor, eps: float, scale: float) -> Tensor:
         query = _contiguous(query)
         # always saved: the accumulating kernels read the refinement
-        out, out_refine, logit, inv_rms, stats = sources_forward_impl(list(bank.sources), query, eps, scale, True)
+        out, out_refine, logit, inv_rms, stats = sources_forward_impl(list(bank.sources), query, eps, scale, True,
+                                                                      pooled=True)
         ctx.bank = bank
         ctx.scale = scale
         ctx.token_device = token.device
@@ -221,7 +229,7 @@ class _BankState:
         grad_out = _contiguous(grad_out.to(torch.bfloat16))
         saved = (_contiguous(out).data_ptr(), _contiguous(out_refine).data_ptr(), grad_out.data_ptr(),
                  _contiguous(logit).data_ptr(), _contiguous(inv_rms).data_ptr(), _contiguous(stats).data_ptr())
-        with torch.cuda.device(device):
+        with _on_device(device):
             if self._prefix(slots):
                 status = lib.attnres_hip_packed_backward_accumulate_f32(
                     self._values.data_ptr(), tokens * width, width, count, tokens, width, query.data_ptr(), rank,
@@ -255,7 +263,7 @@ class _BankState:
         grad_out = _contiguous(grad_out.to(torch.bfloat16))
         saved = (_contiguous(out).data_ptr(), _contiguous(out_refine).data_ptr(), grad_out.data_ptr(),
                  _contiguous(logit).data_ptr(), _contiguous(inv_rms).data_ptr(), _contiguous(stats).data_ptr())
-        with torch.cuda.device(device):
+        with _on_device(device):
             if self._prefix(slots):
                 status = lib.attnres_hip_packed_backward_coef(
                     self._values.data_ptr(), tokens * width, width, count, tokens, width, query.data_ptr(), rank,
@@ -273,7 +281,9 @@ class _BankState:
         else:  # the query is aligned to the row's last R elements, zeros before
             query_row = torch.zeros((width,), device=device, dtype=torch.bfloat16)
             query_row[width - rank:] = query.reshape(-1)
-        record = (grad_out, query_row, coef, count, rank)
+        # the tensors stay referenced until the slots' gathers are enqueued
+        record = ((grad_out, query_row, coef), (grad_out.data_ptr(), query_row.data_ptr(), coef.data_ptr(), count),
+                  rank)
         for position, slot in enumerate(slots):
             self._pending[slot].append((record, position))
         return grad_query
@@ -294,14 +304,16 @@ class _BankState:
         lib = _native.load()
         width = int(self._values.shape[-1])
         tokens = self._values[0].numel() // width
-        reads = (_GatherRead * len(pending))()
-        for entry, ((grad_out, query_row, coef, count, rank), position) in zip(reads, pending):
-            entry.grad_out, entry.query_row, entry.coef = grad_out.data_ptr(), query_row.data_ptr(), coef.data_ptr()
-            entry.n_sources, entry.position, entry.rank = count, position, rank
+        reads = array("q")  # attnres_gather_read[len(pending)]
+        for (_, head, rank), position in pending:
+            reads.extend(head)
+            reads.append(position)
+            reads.append(rank)
         grad = torch.empty(self._values.shape[1:], device=self._values.device, dtype=torch.float32)
-        with torch.cuda.device(self._values.device):
-            status = lib.attnres_hip_bank_gather(self._values[slot].data_ptr(), width, tokens, width, reads,
-                                                 len(pending), grad.data_ptr(), 0, _stream(self._values.device))
+        with _on_device(self._values.device):
+            status = lib.attnres_hip_bank_gather(self._values[slot].data_ptr(), width, tokens, width,
+                                                 reads.buffer_info()[0], len(pending), grad.data_ptr(), 0,
+                                                 _stream(self._values.device))
         _native.check(status, "attnres source-bank gather")
         return grad
 
@@ -469,7 +481,7 @@ class _PushSum(torch.autograd.Function):
         prev, emitted = _contiguous(prev.detach()), _contiguous(emitted.detach())
         partial = torch.empty_like(emitted)
         dtype = _DTYPE_F32 if emitted.dtype == torch.float32 else _DTYPE_BF16
-        with torch.cuda.device(emitted.device):
+        with _on_device(emitted.device):
             status = lib.attnres_hip_partial_sum(prev.data_ptr(), emitted.data_ptr(), dtype, emitted.numel(),
                                                  partial.data_ptr(), bank._values[slot].data_ptr(),
                                                  _stream(emitted.device))
@@ -495,10 +507,10 @@ class _BankRead(torch.autograd.Function):
         shape = bank._values.shape[1:]
         if bank._prefix(slots):
             flat = bank._values[:len(slots)].reshape(len(slots), -1, shape[-1])  # a view: the bank is contiguous
-            out, out_refine, logit, inv_rms, stats = packed_forward_impl(flat, query, eps, scale, True)
+            out, out_refine, logit, inv_rms, stats = packed_forward_impl(flat, query, eps, scale, True, pooled=True)
         else:
             out, out_refine, logit, inv_rms, stats = sources_forward_impl(bank._sources(slots), query, eps, scale,
-                                                                         True)
+                                                                         True, pooled=True)
         # always saved: the accumulating kernels read the refinement
         ctx.bank, ctx.slots, ctx.scale = bank, slots, scale
         ctx.token_device = token.device

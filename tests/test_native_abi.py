@@ -222,6 +222,13 @@ def test_gather_read_struct_matches_the_header():
     fields = re.findall(r"^\s*[\w\s\*]+?\b(\w+);", re.sub(r"/\*.*?\*/", "", body.group(1), flags=re.S), re.M)
     assert fields == [name for name, _ in _GatherRead._fields_]
     assert ctypes.sizeof(_GatherRead) == 6 * 8
+    # the source bank passes the table as an int64 array of the same bytes
+    from array import array
+
+    rows = [(0x7F0000001000, 0x7F0000002000, 0x7F0000003000, 5, 2, 384), (16, 32, 48, 1, 0, 1)]
+    table = (_GatherRead * 2)(*rows)
+    packed = array("q", [field for row in rows for field in row])
+    assert bytes(table) == packed.tobytes()
 
 
 def test_coefficient_backward_and_gather_check_on_the_host():
@@ -251,4 +258,10 @@ def test_coefficient_backward_and_gather_check_on_the_host():
     assert b"position" in lib.attnres_hip_last_error()
     reads[1].position, reads[1].coef = 2, None
     assert lib.attnres_hip_bank_gather(_FAKE, 64, 4, 64, reads, 2, _FAKE, 0, None) == _native.ERR_NULL_POINTER
+    from array import array
+
+    packed = array("q", bytes(reads))  # the source bank's form of the table: the same checks apply
+    packed[3 + 6] = 4  # read 1: n_sources 3 -> 4, so position 2 is in range but coef is still NULL
+    assert lib.attnres_hip_bank_gather(_FAKE, 64, 4, 64, packed.buffer_info()[0], 2, _FAKE, 0,
+                                       None) == _native.ERR_NULL_POINTER
     assert lib.attnres_hip_bank_gather(_FAKE, 64, 4, 64, reads, 0, _FAKE, 0, None) == _native.ERR_SHAPE
