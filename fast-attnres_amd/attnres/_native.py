@@ -73,7 +73,7 @@ SIGNATURES = {
         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
         _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p]),
     "attnres_hip_bank_gather": (ctypes.c_int, [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _c_void_p, ctypes.c_int,
-                                               _c_void_p]),
+                                               ctypes.c_int, _c_void_p]),
     "attnres_hip_partial_sum": (ctypes.c_int, [_c_void_p, _c_void_p, ctypes.c_int, _i64, _c_void_p, _c_void_p,
                                                _c_void_p]),
 }

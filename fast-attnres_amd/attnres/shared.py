@@ -50,6 +50,10 @@ from ._ops import (_contiguous, _dq_workspace, _on_device, _source_table, _strea
 from ._sources import _EPS, _MAX_SOURCES, _MAX_WIDTH, check_query, check_sources
 
 _DTYPE_F32, _DTYPE_BF16 = 0, 1  # attnres_hip.h ATTNRES_DTYPE_*
+_MAX_GATHER_READS = 48  # attnres_hip.h ATTNRES_MAX_GATHER_READS
+# A BF16 source's gathered gradient is stored as BF16 by the gather itself
+# when one launch covers its reads (else FP32, converted afterwards).
+_BF16_GATHER = True
 
 
 class _GatherRead(ctypes.Structure):
@@ -288,9 +292,10 @@ class _BankState:
             self._pending[slot].append((record, position))
         return grad_query
 
-    def _take(self, slot: int) -> Tensor | None:
-        """Slot `slot`'s FP32 gradient for this pass (gathered, or a view of the
-        accumulated sums), or None."""
+    def _take(self, slot: int, dtype: torch.dtype) -> Tensor | None:
+        """Slot `slot`'s gradient for this pass, or None: gathered (in BF16
+        when ``dtype`` is BF16 and one gather launch covers the slot's reads,
+        else FP32), or a view of the FP32 accumulated sums."""
         if self._pass != _pass_id():
             return None
         if self.gradients == "accumulate":
@@ -309,10 +314,15 @@ class _BankState:
             reads.extend(head)
             reads.append(position)
             reads.append(rank)
-        grad = torch.empty(self._values.shape[1:], device=self._values.device, dtype=torch.float32)
+        rank0 = pending[0][0][2]
+        bf16 = (_BF16_GATHER and dtype == torch.bfloat16 and len(pending) <= _MAX_GATHER_READS
+                and all(rank == rank0 for (_, _, rank), _ in pending))
+        grad = torch.empty(self._values.shape[1:], device=self._values.device,
+                           dtype=torch.bfloat16 if bf16 else torch.float32)
         with _on_device(self._values.device):
             status = lib.attnres_hip_bank_gather(self._values[slot].data_ptr(), width, tokens, width,
-                                                 reads.buffer_info()[0], len(pending), grad.data_ptr(), 0,
+                                                 reads.buffer_info()[0], len(pending), grad.data_ptr(),
+                                                 _DTYPE_BF16 if bf16 else _DTYPE_F32, 0,
                                                  _stream(self._values.device))
         _native.check(status, "attnres source-bank gather")
         return grad
@@ -466,7 +476,7 @@ class _Push(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, _token_grad):
-        grad = ctx.bank._take(ctx.slot)
+        grad = ctx.bank._take(ctx.slot, ctx.dtype)
         return None, None, None if grad is None else grad.to(ctx.dtype), _token_input_grad(ctx, 3)
 
 
@@ -491,7 +501,7 @@ class _PushSum(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_partial, _token_grad):
-        grad = ctx.bank._take(ctx.slot)
+        grad = ctx.bank._take(ctx.slot, ctx.dtype)
         if grad is not None:
             grad = grad.to(ctx.dtype) if grad_partial is None else grad_partial + grad.to(ctx.dtype)
         else:

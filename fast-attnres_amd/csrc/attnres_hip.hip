@@ -658,13 +658,24 @@ int attnres_hip_sources_backward_coef(const void* const* sources, const int64_t*
 }
 
 int attnres_hip_bank_gather(const void* values, int64_t row_stride, int64_t n_tokens, int64_t width,
-                            const attnres_gather_read* reads, int64_t n_reads, float* grad, int accumulate,
-                            void* stream) {
+                            const attnres_gather_read* reads, int64_t n_reads, void* grad, int grad_dtype,
+                            int accumulate, void* stream) {
   int st = check_shape(1, n_tokens, width, 1);
   if (st) return st;
   if (!values || !reads || !grad) return fail(ATTNRES_ERR_NULL_POINTER, "null pointer argument to attnres_hip_bank_gather");
   if (row_stride < 0) return fail(ATTNRES_ERR_STRIDE, "negative row stride");
   if (n_reads < 1) return fail(ATTNRES_ERR_SHAPE, "n_reads=%lld must be positive", (long long)n_reads);
+  if (grad_dtype != ATTNRES_DTYPE_F32 && grad_dtype != ATTNRES_DTYPE_BF16)
+    return fail(ATTNRES_ERR_SHAPE, "grad_dtype=%d is neither ATTNRES_DTYPE_F32 nor ATTNRES_DTYPE_BF16", grad_dtype);
+  const bool bf16_out = grad_dtype == ATTNRES_DTYPE_BF16;
+  if (bf16_out) {  // one launch, so that the sum is rounded once
+    bool one_rank = true;
+    for (int64_t r = 1; r < n_reads; ++r) one_rank = one_rank && reads[r].rank == reads[0].rank;
+    if (accumulate || n_reads > ATTNRES_MAX_GATHER_READS || !one_rank)
+      return fail(ATTNRES_ERR_SHAPE,
+                  "a BF16 gradient is written by one launch: accumulate=0, at most %d reads, all of one rank",
+                  ATTNRES_MAX_GATHER_READS);
+  }
   bool vec = width % kVec == 0 && aligned16(values) && aligned16(grad) && (row_stride % kVec == 0 || n_tokens == 1);
   for (int64_t r = 0; r < n_reads; ++r) {
     const attnres_gather_read& rd = reads[r];
@@ -690,6 +701,7 @@ int attnres_hip_bank_gather(const void* values, int64_t row_stride, int64_t n_to
     a.width = static_cast<int>(width);
     a.tail0 = static_cast<int>(width - reads[first].rank);
     a.accumulate = (accumulate || !first_launch) ? 1 : 0;
+    a.bf16_out = bf16_out ? 1 : 0;
     int count = 0;
     while (first + count < n_reads && count < kMaxGatherReads && reads[first + count].rank == reads[first].rank) {
       const attnres_gather_read& rd = reads[first + count];

@@ -140,7 +140,8 @@ struct BwdArgs {
 };
 
 // One read that saw the slot being gathered (see attnres_hip_bank_gather).
-constexpr int kMaxGatherReads = 48;  // per launch; more reads take further, accumulating launches
+constexpr int kMaxGatherReads = ATTNRES_MAX_GATHER_READS;  // per launch; more reads take further,
+                                                           // accumulating launches
 struct GatherRead {
   const uint16_t* grad_out;  // [N, D] BF16 dO of the read
   const uint16_t* qrow;      // [D] BF16: the query on the read's key coordinates, 0 before them
@@ -154,12 +155,13 @@ struct GatherRead {
 struct GatherArgs {
   const uint16_t* values;  // the slot's [N, D] BF16 rows (row n at values + n * row_stride)
   int64_t row_stride;
-  float* grad;             // [N, D] FP32, contiguous
+  void* grad;              // [N, D] contiguous: FP32, or BF16 when bf16_out
   int64_t n_tokens;
   int width;
   int tail0;
   int n_reads;
-  int accumulate;          // 1: add to grad, 0: write it
+  int accumulate;          // 1: add to grad (FP32 only), 0: write it
+  int bf16_out;            // 1: store the FP32 sums rounded to BF16 (one launch, no accumulate)
   GatherRead read[kMaxGatherReads];
 };
 
@@ -240,7 +242,7 @@ int64_t launch_bwd_recompute_geometry(const BwdArgs<Rows, Grads>& a, bool nomask
 template <int G, int CH, class Rows>
 int64_t launch_bwd_geometry_coef(const BwdArgs<Rows, CoefSink>& a, bool nomask, bool vec, hipStream_t stream);
 template <int G, int CH>
-void launch_gather_geometry(const GatherArgs& a, bool vec, hipStream_t stream);
+void launch_gather_geometry(const GatherArgs& a, bool vec, hipStream_t stream);  // bf16_out read from a
 
 #define ATTNRES_DECLARE_GEOMETRY_COEF(G, CH)                                                                 \
   extern template int64_t launch_bwd_geometry_coef<G, CH, PackedRows>(const BwdArgs<PackedRows, CoefSink>&, \

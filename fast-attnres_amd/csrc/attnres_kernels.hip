@@ -1036,7 +1036,9 @@ __global__ void __launch_bounds__(kBlock) attnres_bwd_recompute_kernel(const Bwd
 // blocks), so each read's query row is loaded once per T tokens and its
 // coefficients for the T tokens are contiguous.  A ring of kRing reads keeps
 // the next reads' rows in flight while one is added.
-template <int G, int CH, bool VEC>
+// BF16OUT: the sums are stored rounded to BF16 (round to nearest even), for a
+// BF16 source, instead of an FP32 row converted by a separate pass.
+template <int G, int CH, bool VEC, bool BF16OUT>
 __global__ void __launch_bounds__(kBlock) attnres_gather_kernel(const GatherArgs a) {
   static_assert(kBlock % G == 0 && (G <= 64 || G % 64 == 0), "groups of whole wavefronts above 64 lanes");
   constexpr int T = CH >= 4 ? 1 : 4 / CH;      // tokens per group iteration
@@ -1111,7 +1113,6 @@ __global__ void __launch_bounds__(kBlock) attnres_gather_kernel(const GatherArgs
       if (token0 + t >= N) break;  // uniform
       u32x4 v[CH];
       load_row<G, CH, VEC>(a.values + tok[t] * a.row_stride, lane, D, v);
-      float* grad_row = a.grad + tok[t] * D;
 #pragma unroll
       for (int c = 0; c < CH; ++c) {
         const int d0 = chunk_start<G>(c, lane);
@@ -1122,6 +1123,14 @@ __global__ void __launch_bounds__(kBlock) attnres_gather_kernel(const GatherArgs
           acc[t][c][2 * k] = fmaf(d >= a.tail0 ? bsum[t] : 0.0f, bf16_lo(vw[k]), acc[t][c][2 * k]);
           acc[t][c][2 * k + 1] = fmaf(d + 1 >= a.tail0 ? bsum[t] : 0.0f, bf16_hi(vw[k]), acc[t][c][2 * k + 1]);
         }
+        if constexpr (BF16OUT) {
+          uint16_t* grad_row = static_cast<uint16_t*>(a.grad) + tok[t] * D;
+          const u32x4 packed{pack_bf16x2(acc[t][c][0], acc[t][c][1]), pack_bf16x2(acc[t][c][2], acc[t][c][3]),
+                             pack_bf16x2(acc[t][c][4], acc[t][c][5]), pack_bf16x2(acc[t][c][6], acc[t][c][7])};
+          if (d0 < D) store_chunk<VEC>(grad_row, d0, D, packed);
+          continue;
+        }
+        float* grad_row = static_cast<float*>(a.grad) + tok[t] * D;
         if (a.accumulate) {  // uniform
 #pragma unroll
           for (int e = 0; e < kVec; ++e) acc[t][c][e] += grad_row[min(d0 + e, D - 1)];
@@ -1271,6 +1280,14 @@ int64_t launch_bwd_geometry_coef(const BwdArgs<Rows, CoefSink>& a, bool nomask, 
   return launch_bwd_variant<G, CH, false>(a, nomask, vec, stream);
 }
 
+template <int G, int CH, bool VEC, bool BF16OUT>
+void launch_gather(const GatherArgs& a, hipStream_t stream) {
+  const int64_t blocks =
+      grid_blocks(a.n_tokens, a.width, resident_blocks<&attnres_gather_kernel<G, CH, VEC, BF16OUT>>());
+  hipLaunchKernelGGL((attnres_gather_kernel<G, CH, VEC, BF16OUT>), dim3(static_cast<unsigned>(blocks)),
+                     dim3(kBlock), 0, stream, a);
+}
+
 // The gather has no group sums, so a row is spread over up to a whole
 // workgroup with as few chunks per lane as the width allows (fewer registers:
 // 64 lanes x 4 chunks took 204 VGPRs, 256 x 1 far fewer).
@@ -1280,15 +1297,11 @@ void launch_gather_geometry(const GatherArgs& a, bool vec, hipStream_t stream) {
   constexpr int kChunks = G * CH / kLanes;
   static_assert(kLanes * kChunks == G * CH, "same row coverage");
   if (vec) {
-    const int64_t blocks =
-        grid_blocks(a.n_tokens, a.width, resident_blocks<&attnres_gather_kernel<kLanes, kChunks, true>>());
-    hipLaunchKernelGGL((attnres_gather_kernel<kLanes, kChunks, true>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(kBlock), 0, stream, a);
+    if (a.bf16_out) launch_gather<kLanes, kChunks, true, true>(a, stream);
+    else launch_gather<kLanes, kChunks, true, false>(a, stream);
   } else {
-    const int64_t blocks =
-        grid_blocks(a.n_tokens, a.width, resident_blocks<&attnres_gather_kernel<kLanes, kChunks, false>>());
-    hipLaunchKernelGGL((attnres_gather_kernel<kLanes, kChunks, false>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(kBlock), 0, stream, a);
+    if (a.bf16_out) launch_gather<kLanes, kChunks, false, true>(a, stream);
+    else launch_gather<kLanes, kChunks, false, false>(a, stream);
   }
 }
 

@@ -69,9 +69,11 @@ enum attnres_status {
 /* Reads of at most this many sources may skip the refinement (see above). */
 #define ATTNRES_RECOMPUTE_MAX_SOURCES 3
 
-/* Element types of attnres_hip_partial_sum. */
+/* Element types of attnres_hip_partial_sum and attnres_hip_bank_gather. */
 #define ATTNRES_DTYPE_F32 0
 #define ATTNRES_DTYPE_BF16 1
+/* Reads one attnres_hip_bank_gather launch takes (more take further launches). */
+#define ATTNRES_MAX_GATHER_READS 48
 
 /* Library version string, e.g. "1.0.0". */
 const char* attnres_hip_version(void);
@@ -305,13 +307,18 @@ typedef struct attnres_gather_read {
  * with p, a, b of read r at token n from its coefficient backward -- the
  * read's own dv, summed over the reads in FP32.
  * `values` are the source's BF16 rows (row n at values + n*row_stride), grad
- * is contiguous FP32 [N, D]; accumulate != 0 adds to it.  One pass over the
- * dO rows instead of one read-modify-write of an FP32 sum per read.  No
- * counterpart in the reference; used by attnres.SourceBank.
+ * is contiguous [N, D] of `grad_dtype`: ATTNRES_DTYPE_F32 (accumulate != 0
+ * adds to it), or ATTNRES_DTYPE_BF16 -- the FP32 sum rounded once to BF16
+ * (nearest even), for a BF16 source; this needs one launch: accumulate == 0,
+ * at most ATTNRES_MAX_GATHER_READS reads, all of one rank (else
+ * ATTNRES_ERR_SHAPE).  One pass over the dO rows instead of one
+ * read-modify-write of an FP32 sum per read.  No counterpart in the
+ * reference; used by attnres.SourceBank.
  */
 int attnres_hip_bank_gather(const void* values, int64_t row_stride, int64_t n_tokens,
                             int64_t width, const attnres_gather_read* reads,
-                            int64_t n_reads, float* grad, int accumulate, void* stream);
+                            int64_t n_reads, void* grad, int grad_dtype, int accumulate,
+                            void* stream);
 
 /*
  * Block-schedule partial sum: out[i] = prev[i] + emitted[i] (FP32 arithmetic,

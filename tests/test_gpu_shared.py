@@ -362,3 +362,38 @@ def test_banks_free_their_buffers_with_the_graph():
         assert torch.cuda.memory_allocated() == before
     finally:
         gc.enable()
+
+
+@pytest.mark.parametrize("width,rank,reads", [(1024, 1024, 4), (1003, 96, 4), (4096, 4096, 3), (256, 256, 50)],
+                         ids=["d1024", "d1003_r96_unaligned", "d4096", "d256_50_reads"])
+def test_bf16_gathered_gradients_equal_the_converted_fp32_sums(width, rank, reads, monkeypatch):
+    """BF16 sources: the gather stores the gradient as BF16 itself, which is
+    bit-identical to the FP32 gather converted by torch (both round the same
+    FP32 sum once, to nearest even).  With 50 reads slot 0 needs two gather
+    launches, so it takes the FP32 path and the conversion in both runs."""
+    from attnres import SourceBank, shared
+
+    torch.manual_seed(53)
+    embedded = torch.randn(3, 41, width, device="cuda").to(torch.bfloat16).requires_grad_()
+    weights = [torch.randn(width, width, device="cuda") / math.sqrt(width) for _ in range(min(reads, 4))]
+    queries = [(torch.randn(rank, device="cuda") / math.sqrt(rank)).to(torch.bfloat16).requires_grad_()
+               for _ in range(reads)]
+    grads = [torch.randn(3, 41, width, device="cuda").to(torch.bfloat16) for _ in range(reads)]
+    print(f"bf16 gather width={width} rank={rank} reads={reads}", flush=True)
+
+    def run():
+        bank = SourceBank(reads + 1)
+        bank.push(embedded)
+        outs = []
+        for i, query in enumerate(queries):
+            x = bank.read(query)
+            outs.append(x)
+            bank.push(torch.tanh(x.float() @ weights[i % len(weights)]).to(torch.bfloat16))
+        return torch.autograd.grad(outs, (embedded, *queries), grads)
+
+    direct = run()
+    monkeypatch.setattr(shared, "_BF16_GATHER", False)
+    converted = run()
+    assert direct[0].dtype == torch.bfloat16
+    for a, b in zip(direct, converted):
+        assert torch.equal(a, b)

@@ -195,6 +195,9 @@ def test_partial_sum_checks_its_arguments_on_the_host():
     assert lib.attnres_hip_partial_sum(_FAKE, _FAKE, 0, 0, _FAKE, _FAKE, None) == _native.ERR_SHAPE
     text = HEADER.read_text()
     assert "#define ATTNRES_DTYPE_F32 0" in text and "#define ATTNRES_DTYPE_BF16 1" in text
+    from attnres import shared
+
+    assert f"#define ATTNRES_MAX_GATHER_READS {shared._MAX_GATHER_READS}" in text
 
 
 def test_list_f32_accumulating_backward_checks_like_the_others():
@@ -254,14 +257,26 @@ def test_coefficient_backward_and_gather_check_on_the_host():
         entry.grad_out = entry.query_row = entry.coef = _FAKE
         entry.n_sources, entry.position, entry.rank = 3, 1, 16
     reads[1].position = 3
-    assert lib.attnres_hip_bank_gather(_FAKE, 64, 4, 64, reads, 2, _FAKE, 0, None) == _native.ERR_SHAPE
+    assert lib.attnres_hip_bank_gather(_FAKE, 64, 4, 64, reads, 2, _FAKE, 0, 0, None) == _native.ERR_SHAPE
     assert b"position" in lib.attnres_hip_last_error()
     reads[1].position, reads[1].coef = 2, None
-    assert lib.attnres_hip_bank_gather(_FAKE, 64, 4, 64, reads, 2, _FAKE, 0, None) == _native.ERR_NULL_POINTER
+    assert lib.attnres_hip_bank_gather(_FAKE, 64, 4, 64, reads, 2, _FAKE, 0, 0, None) == _native.ERR_NULL_POINTER
     from array import array
 
     packed = array("q", bytes(reads))  # the source bank's form of the table: the same checks apply
     packed[3 + 6] = 4  # read 1: n_sources 3 -> 4, so position 2 is in range but coef is still NULL
-    assert lib.attnres_hip_bank_gather(_FAKE, 64, 4, 64, packed.buffer_info()[0], 2, _FAKE, 0,
+    assert lib.attnres_hip_bank_gather(_FAKE, 64, 4, 64, packed.buffer_info()[0], 2, _FAKE, 0, 0,
                                        None) == _native.ERR_NULL_POINTER
-    assert lib.attnres_hip_bank_gather(_FAKE, 64, 4, 64, reads, 0, _FAKE, 0, None) == _native.ERR_SHAPE
+    assert lib.attnres_hip_bank_gather(_FAKE, 64, 4, 64, reads, 0, _FAKE, 0, 0, None) == _native.ERR_SHAPE
+    # BF16 output: a known element type, written by one launch (every case fails before any launch)
+    reads[1].coef = _FAKE
+    assert lib.attnres_hip_bank_gather(_FAKE, 64, 4, 64, reads, 2, _FAKE, 7, 0, None) == _native.ERR_SHAPE
+    assert b"grad_dtype" in lib.attnres_hip_last_error()
+    bf16 = 1
+    assert lib.attnres_hip_bank_gather(_FAKE, 64, 4, 64, reads, 2, _FAKE, bf16, 1, None) == _native.ERR_SHAPE
+    assert b"one launch" in lib.attnres_hip_last_error()
+    reads[1].rank = 32
+    assert lib.attnres_hip_bank_gather(_FAKE, 64, 4, 64, reads, 2, _FAKE, bf16, 0, None) == _native.ERR_SHAPE
+    many = (_GatherRead * 49)(*[(_FAKE, _FAKE, _FAKE, 3, 0, 16)] * 49)
+    assert lib.attnres_hip_bank_gather(_FAKE, 64, 4, 64, many, 49, _FAKE, bf16, 0, None) == _native.ERR_SHAPE
+    assert b"at most 48 reads" in lib.attnres_hip_last_error()
