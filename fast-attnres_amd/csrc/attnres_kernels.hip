@@ -1157,12 +1157,45 @@ __global__ void __launch_bounds__(kBlock) attnres_gather_kernel(const GatherArgs
 
 // Ring depth (rows in flight per group) for a chunk count.  Measured on
 // MI355X at S=25, D=2048: the forward is equally fast with 3 or 4 rows in
-// flight (2 is slower); the backward is fastest with one row per group,
-// because every further slot costs occupancy.
+// flight (2 is slower).
 template <int CH>
 constexpr int fwd_ring() { return CH <= 4 ? 4 : 2; }
-template <int CH>
-constexpr int bwd_ring() { return 1; }
+
+// Compute units of the current device (cached per device; 0 if unknown).
+inline int64_t device_cus() {
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return 0;
+  static thread_local int cached_device = -1;
+  static thread_local int64_t cached = 0;
+  if (cached_device == device) return cached;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  cached_device = device;
+  cached = cus;
+  return cached;
+}
+
+// Backward ring depth.  One row per group, except two for aligned,
+// non-accumulating rows of 4 chunks (the variants that keep two rows without
+// spilling): at 64 lanes (D <= 2048) and 256 lanes (D > 4096) always, at
+// 32 lanes (D <= 1024) when the grid holds at most 4 wavefronts per CU, where
+// a group has a long chain of items and little else hides its latency.
+// Measured on MI355X (backward, median of 8 interleaved rounds, us):
+// S=25, N=16384, D=2048: 645 -> 637; S=9, N=8192, D=8192: 492 -> 483;
+// S=25, N=2048, D=1024: 54 -> 47 (R=D), 55 -> 48 (R=256); but at N=16384,
+// D=1024 two rows are 0.8% slower (occupancy 2 either way), and the
+// accumulating and element-wise variants spill with two.
+template <int CH, bool VEC, bool ACC>
+constexpr bool kBwdTwoRowVariant = CH == 4 && VEC && !ACC;
+
+// At most 4 wavefronts per CU for N tokens of G lanes each.
+inline bool few_waves(int64_t n_tokens, int G) {
+  const int64_t cus = device_cus();
+  return cus > 0 && n_tokens * G <= 4 * 64 * cus;
+}
 
 // Workgroups of `Kernel` resident on the current device (cached per kernel
 // and device; 0 if the runtime cannot tell).  The kernel is a template
@@ -1222,14 +1255,25 @@ void launch_fwd_geometry(const FwdArgs<Rows>& a, bool nomask, bool vec, hipStrea
   }
 }
 
-template <int G, int CH, bool NOMASK, bool VEC, bool ACC, class Rows, class Grads>
-int64_t launch_bwd(const BwdArgs<Rows, Grads>& a, hipStream_t stream) {
-  const int64_t resident =
-      resident_blocks<&attnres_bwd_kernel<G, CH, bwd_ring<CH>(), NOMASK, VEC, ACC, Rows, Grads>>();
+template <int G, int CH, int NB, bool NOMASK, bool VEC, bool ACC, class Rows, class Grads>
+int64_t launch_bwd_ring(const BwdArgs<Rows, Grads>& a, hipStream_t stream) {
+  const int64_t resident = resident_blocks<&attnres_bwd_kernel<G, CH, NB, NOMASK, VEC, ACC, Rows, Grads>>();
   const int64_t blocks = grid_blocks(a.n_tokens, a.width, resident);
-  hipLaunchKernelGGL((attnres_bwd_kernel<G, CH, bwd_ring<CH>(), NOMASK, VEC, ACC, Rows, Grads>),
+  hipLaunchKernelGGL((attnres_bwd_kernel<G, CH, NB, NOMASK, VEC, ACC, Rows, Grads>),
                      dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream, a);
   return blocks;
+}
+
+template <int G, int CH, bool NOMASK, bool VEC, bool ACC, class Rows, class Grads>
+int64_t launch_bwd(const BwdArgs<Rows, Grads>& a, hipStream_t stream) {
+  if constexpr (kBwdTwoRowVariant<CH, VEC, ACC> && G >= 64) {
+    return launch_bwd_ring<G, CH, 2, NOMASK, VEC, ACC>(a, stream);
+  } else if constexpr (kBwdTwoRowVariant<CH, VEC, ACC>) {
+    return few_waves(a.n_tokens, G) ? launch_bwd_ring<G, CH, 2, NOMASK, VEC, ACC>(a, stream)
+                                    : launch_bwd_ring<G, CH, 1, NOMASK, VEC, ACC>(a, stream);
+  } else {
+    return launch_bwd_ring<G, CH, 1, NOMASK, VEC, ACC>(a, stream);
+  }
 }
 
 template <int G, int CH, bool ACC, class Rows, class Grads>

@@ -89,6 +89,34 @@ def test_aligned_fast_path_matches_oracle(width, rank, layout):
         compare(a, e)
 
 
+@pytest.mark.parametrize("layout", ["packed", "list"])
+@pytest.mark.parametrize("tokens,width,rank", [(2048, 1024, 1024), (4096, 1024, 1024), (4096, 1024, 256),
+                                               (2048, 1024, 256), (3000, 2048, 512), (64, 8192, 8192)],
+                         ids=lambda v: str(v))
+def test_backward_ring_depths_match_oracle(tokens, width, rank, layout):
+    """The aligned 4-chunk backward keeps two rows per group at D = 1025..2048
+    and above 4096 always, and at D = 513..1024 only on small grids (at most 4
+    wavefronts per CU: N <= 2048 on 256 CUs), one row otherwise: both depths,
+    with and without key masks."""
+    torch.manual_seed(SEEDS[0] + tokens + rank)
+    s = 5
+    values = torch.randn(s, tokens, width, device="cuda", dtype=torch.bfloat16)
+    values = (values * torch.linspace(0.5, 4, s, device="cuda", dtype=torch.bfloat16)[:, None, None])
+    values.requires_grad_()
+    query = (torch.randn(rank, device="cuda", dtype=torch.bfloat16) / math.sqrt(rank)).requires_grad_()
+    upstream = torch.randn(tokens, width, device="cuda", dtype=torch.bfloat16)
+
+    def make(leaves, q):
+        return (tuple(leaves[0].unbind(0)) if layout == "list" else leaves[0]), q
+
+    print(f"ring depths N={tokens} D={width} R={rank} layout={layout}", flush=True)
+    actual = attnres(make([values], query)[0], query)
+    grads = torch.autograd.grad(actual, (values, query), upstream)
+    expected, expected_grads = oracle_grads(make, [values], query, upstream)
+    for a, e in zip((actual, *grads), (expected, *expected_grads)):
+        compare(a, e)
+
+
 @pytest.mark.parametrize("container", ["list", "tuple", "packed_values"])
 def test_source_containers_with_per_source_strides(container):
     """Differently-strided producers, a strided query and a repeated source
