@@ -18,7 +18,7 @@ bandwidth of the whole read in TB/s (bytes below / measured time per read);
     backward = S*N*D*2 (values read) + N*D*2 (dO read) + S*N*D*2 (dvalues write)
 
 ``roofline`` describes the dominant launch, the backward op (the fused
-backward kernel and the two kernels of the deterministic dq reduction),
+backward kernel and the one-launch deterministic dq reduction),
 timed with HIP events recorded on the stream the kernels run on; its
 ``traffic`` is the HBM bytes per launch measured with rocprofv3 counters
 (profiles/attnres_<config>_hbm_traffic.json).  ``cpu_baseline`` times the CPU
@@ -751,8 +751,7 @@ def main(argv=None) -> int:
         "backward": {"us": round(bwd_avg * 1e3, 2), "bytes": bwd_bytes, "TB/s": round(bwd_tbs, 4),
                      "pct_of_peak": round(100 * bwd_tbs / HBM_PEAK_TBS, 2)},
         "roofline": {"bound": "hbm",
-                     "kernel": "backward op: attnres_bwd_kernel + attnres_dq_slices_kernel + "
-                               "attnres_dq_finalize_kernel",
+                     "kernel": "backward op: attnres_bwd_kernel + attnres_dq_reduce_kernel",
                      "achieved": round(bwd_tbs * 1e3, 1), "peak": HBM_PEAK_TBS * 1e3,
                      "unit": "GB/s", "frac": round(bwd_tbs / HBM_PEAK_TBS, 4),
                      "traffic": measured_traffic(args.config, "backward_bytes")},

@@ -49,48 +49,46 @@ __device__ __forceinline__ uint32_t pack2_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
-// The dq reduction is latency-bound (a few MB): each thread issues all of its
-// loads at once (clamped, unconditional indices) and then adds the values in
-// the fixed order, skipping the clamped ones with a select, so the sums are
-// exactly the in-order sums.
-constexpr int kRowsPerSlice = (kMaxGridBlocks + kFinalizeSlices - 1) / kFinalizeSlices;
+// The dq reduction, one launch over the backward's per-block partial rows
+// (a few MB, latency-bound).  Workgroup w owns columns [16w, 16w + 16); its
+// threads are 16 columns x 16 row groups, and row group g sums rows g, g + 16,
+// g + 32, ... in that order, issuing kDqBatch loads at once (clamped,
+// unconditional indices; the clamped values are skipped with a select, so the
+// sums are exactly the in-order sums).  The 16 group sums meet in LDS and are
+// added in group order: a fixed order for a given row count, so dq is
+// bit-reproducible.  Writes the FP32 total and its BF16 copy.
+constexpr int kDqCols = 16;
+constexpr int kDqGroups = kBlock / kDqCols;
+constexpr int kDqBatch = 16;
 
-// First stage of the dq reduction: slice p sums partial rows p, p+P, p+2P, ...
-// (rows <= kMaxGridBlocks and P = min(rows, kFinalizeSlices), so a slice has at
-// most kRowsPerSlice rows).
-__global__ void __launch_bounds__(kBlock) attnres_dq_slices_kernel(
-    const float* __restrict__ partial, int64_t rows, int R, float* __restrict__ slices) {
-  const int col = blockIdx.x * kBlock + threadIdx.x;
-  const int p = blockIdx.y;
-  const int P = gridDim.y;
-  if (col >= R) return;
-  float v[kRowsPerSlice];
-#pragma unroll
-  for (int k = 0; k < kRowsPerSlice; ++k) {
-    const int64_t r = p + static_cast<int64_t>(k) * P;
-    v[k] = partial[(r < rows ? r : p) * R + col];
-  }
-  float t = 0.0f;
-#pragma unroll
-  for (int k = 0; k < kRowsPerSlice; ++k) t = p + static_cast<int64_t>(k) * P < rows ? t + v[k] : t;
-  slices[static_cast<int64_t>(p) * R + col] = t;
-}
-
-// Second stage: dq[r] = sum of the P <= kFinalizeSlices slices in order; FP32
-// total and BF16 copy.
-__global__ void __launch_bounds__(kBlock) attnres_dq_finalize_kernel(
-    const float* __restrict__ slices, int P, int R, float* __restrict__ dq32,
+__global__ void __launch_bounds__(kBlock) attnres_dq_reduce_kernel(
+    const float* __restrict__ partial, int64_t rows, int R, float* __restrict__ dq32,
     uint16_t* __restrict__ dq16) {
-  const int col = blockIdx.x * kBlock + threadIdx.x;
-  if (col >= R) return;
-  float v[kFinalizeSlices];
-#pragma unroll
-  for (int p = 0; p < kFinalizeSlices; ++p) v[p] = slices[static_cast<int64_t>(p < P ? p : 0) * R + col];
+  __shared__ float sums[kDqGroups][kDqCols];
+  const int c = threadIdx.x % kDqCols;
+  const int g = threadIdx.x / kDqCols;
+  const int col = blockIdx.x * kDqCols + c;
+  const int at = col < R ? col : R - 1;
   float t = 0.0f;
+  for (int64_t base = g; base < rows; base += static_cast<int64_t>(kDqGroups) * kDqBatch) {
+    float v[kDqBatch];
 #pragma unroll
-  for (int p = 0; p < kFinalizeSlices; ++p) t = p < P ? t + v[p] : t;
-  dq32[col] = t;
-  dq16[col] = to_bf16(t);
+    for (int k = 0; k < kDqBatch; ++k) {
+      const int64_t r = base + static_cast<int64_t>(k) * kDqGroups;
+      v[k] = partial[(r < rows ? r : base) * R + at];
+    }
+#pragma unroll
+    for (int k = 0; k < kDqBatch; ++k) t = base + static_cast<int64_t>(k) * kDqGroups < rows ? t + v[k] : t;
+  }
+  sums[g][c] = t;
+  __syncthreads();
+  if (g == 0 && col < R) {
+    float total = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kDqGroups; ++k) total += sums[k][c];
+    dq32[col] = total;
+    dq16[col] = to_bf16(total);
+  }
 }
 
 // Block-schedule partial sum: out = prev + emitted in FP32 arithmetic, stored
@@ -215,8 +213,6 @@ int check_shape(int64_t S, int64_t N, int64_t D, int64_t R) {
   return ATTNRES_OK;
 }
 
-int64_t finalize_slices(int64_t rows) { return rows < kFinalizeSlices ? rows : kFinalizeSlices; }
-
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 int launch_status(const char* what) {
@@ -270,8 +266,8 @@ int64_t launch_bwd_select(const BwdArgs<Rows, Grads>& a, bool nomask, bool vec, 
 }
 
 template <class Rows, class Grads>
-int launch_backward(const BwdArgs<Rows, Grads>& a, bool vec, bool acc, bool recompute, float* slices, float* dq32,
-                    uint16_t* dq16, hipStream_t stream) {
+int launch_backward(const BwdArgs<Rows, Grads>& a, bool vec, bool acc, bool recompute, float* dq32, uint16_t* dq16,
+                    hipStream_t stream) {
   const Geometry geo = geometry(a.width);
   const bool nomask = no_mask(geo, a.width, a.rank);
   int64_t blocks = 0;
@@ -286,13 +282,9 @@ int launch_backward(const BwdArgs<Rows, Grads>& a, bool vec, bool acc, bool reco
   }
   int st = launch_status("attnres backward");
   if (st != ATTNRES_OK) return st;
-  const int64_t P = finalize_slices(blocks);
-  const unsigned cols = static_cast<unsigned>((a.rank + kBlock - 1) / kBlock);
-  hipLaunchKernelGGL(attnres_dq_slices_kernel, dim3(cols, static_cast<unsigned>(P)), dim3(kBlock), 0, stream,
-                     a.partial, blocks, a.rank, slices);
-  if ((st = launch_status("attnres dq reduction")) != ATTNRES_OK) return st;
-  hipLaunchKernelGGL(attnres_dq_finalize_kernel, dim3(cols), dim3(kBlock), 0, stream, slices,
-                     static_cast<int>(P), a.rank, dq32, dq16);
+  const unsigned strips = static_cast<unsigned>((a.rank + kDqCols - 1) / kDqCols);
+  hipLaunchKernelGGL(attnres_dq_reduce_kernel, dim3(strips), dim3(kBlock), 0, stream, a.partial, blocks, a.rank,
+                     dq32, dq16);
   return launch_status("attnres dq reduction");
 }
 
@@ -329,10 +321,10 @@ int check_recompute(bool recompute, int64_t S, const char* name) {
   return ATTNRES_OK;
 }
 
-// Workspace layout (FP32): [max_blocks, R] partial rows, [slices, R], [R] total.
+// Workspace layout (FP32): [max_blocks, R] partial rows, [R] total.
 int64_t workspace_elems(int64_t N, int64_t D, int64_t R) {
   const int64_t rows = grid_blocks(N, D, 0);
-  return (rows + finalize_slices(rows) + 1) * R;
+  return (rows + 1) * R;
 }
 
 }  // namespace
@@ -441,10 +433,8 @@ int packed_backward(const void* values, int64_t source_stride, int64_t row_strid
                    aligned16_or_null(out_refine) && aligned16(grad_out) && (kCoef || aligned16(grad_values)) &&
                    (source_stride % kVec == 0 || n_sources == 1) && (row_stride % kVec == 0 || n_tokens == 1);
   const bool acc = set_accumulate(a, accumulate, n_sources);
-  const int64_t rows = grid_blocks(n_tokens, width, 0);
-  float* slices = dq_workspace + rows * rank;
-  float* dq32 = dq_workspace + (need - rank);
-  return launch_backward(a, vec, acc, recompute, slices, dq32, static_cast<uint16_t*>(grad_query),
+  float* dq32 = dq_workspace + (need - rank);  // after the partial rows
+  return launch_backward(a, vec, acc, recompute, dq32, static_cast<uint16_t*>(grad_query),
                          static_cast<hipStream_t>(stream));
 }
 
@@ -584,10 +574,8 @@ int sources_backward(const void* const* sources, const int64_t* row_strides, int
   a.rank = static_cast<int>(rank);
   a.scale = scale;
   const bool acc = set_accumulate(a, accumulate, n_sources);
-  const int64_t rows = grid_blocks(n_tokens, width, 0);
-  float* slices = dq_workspace + rows * rank;
-  float* dq32 = dq_workspace + (need - rank);
-  return launch_backward(a, vec, acc, recompute, slices, dq32, static_cast<uint16_t*>(grad_query),
+  float* dq32 = dq_workspace + (need - rank);  // after the partial rows
+  return launch_backward(a, vec, acc, recompute, dq32, static_cast<uint16_t*>(grad_query),
                          static_cast<hipStream_t>(stream));
 }
 

@@ -21,7 +21,6 @@ constexpr int kMaxWidth = ATTNRES_MAX_WIDTH;
 constexpr int kBlock = 256;           // threads per workgroup (4 wavefronts)
 constexpr int kVec = 8;               // BF16 elements per chunk (16 bytes)
 constexpr int kMaxGridBlocks = 2048;  // persistent grid cap
-constexpr int kFinalizeSlices = 64;   // first-stage slices of the dq reduction
 // Save/recompute policy: reads of at most this many sources save no output
 // refinement; their backward derives delta from the value rows.
 constexpr int kRecomputeMaxSources = ATTNRES_RECOMPUTE_MAX_SOURCES;

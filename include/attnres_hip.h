@@ -108,7 +108,7 @@ int attnres_hip_packed_forward(const void* values, int64_t source_stride,
 
 /*
  * Number of FP32 elements the backward needs in `dq_workspace`
- * (partial dq rows of the deterministic two-stage reduction, plus the FP32
+ * (partial dq rows of the deterministic reduction, one per backward workgroup, plus the FP32
  * total).  Depends only on (n_tokens, width, rank); never negative for
  * in-envelope shapes, -1 otherwise.  Host-only.
  */
