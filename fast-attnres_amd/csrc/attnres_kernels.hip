@@ -1034,15 +1034,15 @@ __global__ void __launch_bounds__(kBlock) attnres_bwd_recompute_kernel(const Bwd
 // of a launch share R, so the b terms meet in one scalar per token.
 // A group takes T consecutive tokens at a time (grid-stride over token
 // blocks), so each read's query row is loaded once per T tokens and its
-// coefficients for the T tokens are contiguous.  A ring of kRing reads keeps
+// coefficients for the T tokens are contiguous.  A ring of RING reads keeps
 // the next reads' rows in flight while one is added.
 // BF16OUT: the sums are stored rounded to BF16 (round to nearest even), for a
 // BF16 source, instead of an FP32 row converted by a separate pass.
-template <int G, int CH, bool VEC, bool BF16OUT>
+template <int G, int CH, bool VEC, bool BF16OUT, int RING>
 __global__ void __launch_bounds__(kBlock) attnres_gather_kernel(const GatherArgs a) {
   static_assert(kBlock % G == 0 && (G <= 64 || G % 64 == 0), "groups of whole wavefronts above 64 lanes");
   constexpr int T = CH >= 4 ? 1 : 4 / CH;      // tokens per group iteration
-  constexpr int kRing = 2;                     // reads in flight per group (T rows each)
+  constexpr int kRing = RING;                  // reads in flight per group (T rows each)
   constexpr int kGroups = kBlock / G;
   const int lane = threadIdx.x % G;
   const int group = group_index<G>();
@@ -1324,12 +1324,27 @@ int64_t launch_bwd_geometry_coef(const BwdArgs<Rows, CoefSink>& a, bool nomask, 
   return launch_bwd_variant<G, CH, false>(a, nomask, vec, stream);
 }
 
+template <int G, int CH, bool VEC, bool BF16OUT, int RING>
+void launch_gather_ring(const GatherArgs& a, hipStream_t stream) {
+  const int64_t blocks =
+      grid_blocks(a.n_tokens, a.width, resident_blocks<&attnres_gather_kernel<G, CH, VEC, BF16OUT, RING>>());
+  hipLaunchKernelGGL((attnres_gather_kernel<G, CH, VEC, BF16OUT, RING>), dim3(static_cast<unsigned>(blocks)),
+                     dim3(kBlock), 0, stream, a);
+}
+
+// Gather ring depth: two reads in flight per group, three on small grids
+// (at most 4 wavefronts per CU) with at least 16 reads.  Measured on MI355X
+// (N tokens, D = 1024, us, two -> three): N = 2048: 48 reads 38.4 -> 34.9,
+// 25 reads 22.7 -> 21.4, 8 reads 11.1 -> 11.7; N = 16384, 25 reads:
+// 157.7 -> 165.9.
 template <int G, int CH, bool VEC, bool BF16OUT>
 void launch_gather(const GatherArgs& a, hipStream_t stream) {
-  const int64_t blocks =
-      grid_blocks(a.n_tokens, a.width, resident_blocks<&attnres_gather_kernel<G, CH, VEC, BF16OUT>>());
-  hipLaunchKernelGGL((attnres_gather_kernel<G, CH, VEC, BF16OUT>), dim3(static_cast<unsigned>(blocks)),
-                     dim3(kBlock), 0, stream, a);
+  constexpr int T = CH >= 4 ? 1 : 4 / CH;
+  if (a.n_reads >= 16 && few_waves((a.n_tokens + T - 1) / T, G)) {
+    launch_gather_ring<G, CH, VEC, BF16OUT, 3>(a, stream);
+  } else {
+    launch_gather_ring<G, CH, VEC, BF16OUT, 2>(a, stream);
+  }
 }
 
 // The gather has no group sums, so a row is spread over up to a whole

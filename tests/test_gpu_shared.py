@@ -93,12 +93,12 @@ def test_unused_reads_and_sources_without_grad():
     assert torch.equal(g0, r0) and torch.equal(g2, r2) and torch.equal(gq, rq)
 
 
-def _stream_case(width, rank, events=4, seed=41):
+def _stream_case(width, rank, events=4, seed=41, tokens=37):
     torch.manual_seed(seed)
-    embedded = torch.randn(2, 37, width, device="cuda", requires_grad=True)
+    embedded = torch.randn(2, tokens, width, device="cuda", requires_grad=True)
     weights = [torch.randn(width, width, device="cuda") / math.sqrt(width) for _ in range(events)]
     queries = [(torch.randn(rank, device="cuda") / math.sqrt(rank)).requires_grad_() for _ in range(events)]
-    grads = [torch.randn(2, 37, width, device="cuda") for _ in range(events)]
+    grads = [torch.randn(2, tokens, width, device="cuda") for _ in range(events)]
     return embedded, weights, queries, grads
 
 
@@ -397,3 +397,27 @@ def test_bf16_gathered_gradients_equal_the_converted_fp32_sums(width, rank, read
     assert direct[0].dtype == torch.bfloat16
     for a, b in zip(direct, converted):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("gradients", ["gather", "accumulate"])
+def test_source_bank_on_a_large_grid_matches_the_plain_stream(gradients):
+    """N = 4200 tokens at D = 1024: more than 4 wavefronts per CU, so the
+    32-lane coefficient backward keeps one row per group (small grids keep
+    two); same comparison as the small stream."""
+    from attnres import SourceBank
+
+    embedded, weights, queries, grads = _stream_case(1024, 1024, tokens=2100)
+    print(f"source bank large grid gradients={gradients}", flush=True)
+    bank = SourceBank(len(weights) + 1, gradients=gradients)
+    outs_bank = _run_stream(lambda q: bank.read(q.to(torch.bfloat16)).float(), bank.push, embedded, weights, queries)
+    sources = []
+    outs_ref = _run_stream(
+        lambda q: attnres(torch.stack([s.to(torch.bfloat16) for s in sources]), q.to(torch.bfloat16)).float(),
+        sources.append, embedded, weights, queries)
+    for a, b in zip(outs_bank, outs_ref):
+        assert torch.equal(a, b)
+    params = (embedded, *queries)
+    g_bank = torch.autograd.grad(outs_bank, params, grads)
+    g_ref = torch.autograd.grad(outs_ref, params, grads)
+    for a, b in zip(g_bank, g_ref):
+        torch.testing.assert_close(a, b, rtol=2.0**-6, atol=2.0**-6 * float(b.abs().max()))
