@@ -2,7 +2,7 @@
 //
 // Host-side argument checks, dispatch to the kernels of the row geometry
 // (attnres_kernels.hip, one translation unit per geometry) and the
-// deterministic two-stage reduction of the dq partial rows.  Nothing here
+// deterministic one-launch reduction of the dq partial rows.  Nothing here
 // allocates, synchronises or reads device memory: every entry point only
 // enqueues work on the caller's stream.
 //

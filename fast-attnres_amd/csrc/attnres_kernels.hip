@@ -35,8 +35,10 @@
 //     dv = p dO + [key coords] (a q + b v),  a = scale dz / r,  b = -dz z / (R r^2)
 // folded in FP32 and stored once as BF16.  dq = sum scale dz k accumulates in
 // registers; each workgroup reduces its groups in LDS in a fixed order to
-// one partial row, and two small kernels sum the partial rows in a fixed
-// order, so dq is bit-reproducible run to run.
+// one partial row, and one small kernel sums the partial rows in a fixed
+// order, so dq is bit-reproducible run to run.  The ring holds one value row
+// per group, or two for aligned 4-chunk rows where that does not spill (see
+// launch_bwd).
 //
 // Variants of the backward.  For S <= 3 (the save/recompute policy) a group
 // holds all S rows of its token and takes delta = sum_s p_s dw_s from them,
