@@ -16,6 +16,12 @@ registers ``attnres::_fixed_tail_forward_with_aux`` / ``_fixed_tail_backward``
 * ``sources_backward(sources, query, out, out_refine, grad_out, logit, inv_rms,
   stats, scale)`` -> ``[grad_source_0, ..., grad_source_{S-1}, grad_query]``
 
+In eager mode (not under dynamo tracing, plain tensors) ``packed_attnres``
+and ``sources_attnres`` reach the same launch functions through a direct
+``autograd.Function`` (the same saved state and gradients as the ops'
+registered autograd) instead of the op dispatcher, which costs tens of
+microseconds per read; under ``torch.compile`` they call the ops.
+
 Every output and workspace is allocated here with ``torch.empty`` on the
 caller's device; the kernels run on the current stream and the C ABI never
 allocates or synchronises, so the ops are safe under ``torch.compile``
@@ -191,11 +197,10 @@ def _packed_forward_fake(values, query, eps, scale):
             values.new_empty((2, tokens), dtype=_F32))
 
 
-@torch.library.custom_op("attnres_hip::packed_backward", mutates_args=(),
-                         device_types="cuda", tags=_OP_TAGS)
-def packed_backward(values: Tensor, query: Tensor, out: Tensor, out_refine: Tensor,
-                    grad_out: Tensor, logit: Tensor, inv_rms: Tensor, stats: Tensor,
-                    scale: float) -> tuple[Tensor, Tensor]:
+def packed_backward_impl(values: Tensor, query: Tensor, out: Tensor, out_refine: Tensor,
+                         grad_out: Tensor, logit: Tensor, inv_rms: Tensor, stats: Tensor,
+                         scale: float) -> tuple[Tensor, Tensor]:
+    """The packed backward launch (dv rows and dq)."""
     lib = _native.load()
     values = _unit_feature_stride(values)
     query = _contiguous(query)
@@ -218,6 +223,14 @@ def packed_backward(values: Tensor, query: Tensor, out: Tensor, out_refine: Tens
             workspace.data_ptr(), workspace.numel(), _stream(device))
     _native.check(status, "attnres packed backward")
     return grad_values, grad_query
+
+
+@torch.library.custom_op("attnres_hip::packed_backward", mutates_args=(),
+                         device_types="cuda", tags=_OP_TAGS)
+def packed_backward(values: Tensor, query: Tensor, out: Tensor, out_refine: Tensor,
+                    grad_out: Tensor, logit: Tensor, inv_rms: Tensor, stats: Tensor,
+                    scale: float) -> tuple[Tensor, Tensor]:
+    return packed_backward_impl(values, query, out, out_refine, grad_out, logit, inv_rms, stats, scale)
 
 
 @packed_backward.register_fake
@@ -251,6 +264,35 @@ def _packed_autograd(ctx: Any, grad_out, *_aux_grads):
 packed_forward.register_autograd(_packed_autograd, setup_context=_packed_setup_context)
 
 
+def _eager(*tensors: Tensor) -> bool:
+    """An eager call: not under dynamo tracing, and only plain tensors or
+    parameters (no fake or functional tensors of a compiler's tracing)."""
+    return not torch.compiler.is_compiling() and all(type(t) in (Tensor, torch.nn.Parameter) for t in tensors)
+
+
+class _PackedRead(torch.autograd.Function):
+    """The packed read in eager mode: the same launches, saved state and
+    gradients as the ``packed_forward`` op with its registered autograd, without
+    going through the op dispatcher (tens of microseconds per read, which bound
+    small reads)."""
+
+    @staticmethod
+    def forward(ctx, values: Tensor, query: Tensor, eps: float, scale: float):
+        outputs = packed_forward_impl(values, query, eps, scale, saves_refinement(int(values.shape[0])))
+        _packed_setup_context(ctx, (values, query, eps, scale), outputs)
+        return outputs
+
+    @staticmethod
+    def backward(ctx, grad_out, *_aux_grads):
+        if grad_out is None:
+            return None, None, None, None
+        values, query, out, out_refine, logit, inv_rms, stats = ctx.saved_tensors
+        grad_values, grad_query = packed_backward_impl(values, query, out, out_refine, grad_out, logit, inv_rms,
+                                                       stats, ctx.scale)
+        return (grad_values if ctx.needs_input_grad[0] else None,
+                grad_query if ctx.needs_input_grad[1] else None, None, None)
+
+
 def packed_attnres(values: Tensor, query: Tensor, eps: float, scale: float) -> Tensor:
     """Packed ``[S, ..., D]`` adapter (reference `fixed_tail.fused_attnres`,
     `fixed_tail.py:1097-1135`): flatten the batch axes to ``[S, N, D]`` as a
@@ -260,7 +302,9 @@ def packed_attnres(values: Tensor, query: Tensor, eps: float, scale: float) -> T
     flat = values.reshape(sources, -1, width)
     if width > 1 and flat.stride(2) != 1:
         flat = flat.contiguous()
-    out = packed_forward(flat, _contiguous(query), eps, scale)[0]
+    query = _contiguous(query)
+    read = _PackedRead.apply if _eager(flat, query) else packed_forward
+    out = read(flat, query, eps, scale)[0]
     return out.reshape(values.shape[1:])
 
 
@@ -319,11 +363,10 @@ def _sources_forward_fake(sources, query, eps, scale):
             first.new_empty((2, tokens), dtype=_F32))
 
 
-@torch.library.custom_op("attnres_hip::sources_backward", mutates_args=(),
-                         device_types="cuda", tags=_OP_TAGS)
-def sources_backward(sources: list[Tensor], query: Tensor, out: Tensor, out_refine: Tensor,
-                     grad_out: Tensor, logit: Tensor, inv_rms: Tensor, stats: Tensor,
-                     scale: float) -> list[Tensor]:
+def sources_backward_impl(sources: list[Tensor], query: Tensor, out: Tensor, out_refine: Tensor,
+                          grad_out: Tensor, logit: Tensor, inv_rms: Tensor, stats: Tensor,
+                          scale: float) -> list[Tensor]:
+    """The source-list backward launch: one dv buffer per list position, then dq."""
     lib = _native.load()
     first = sources[0]
     query = _contiguous(query)
@@ -348,6 +391,14 @@ def sources_backward(sources: list[Tensor], query: Tensor, out: Tensor, out_refi
     del prepared
     _native.check(status, "attnres source-list backward")
     return [*grads, grad_query]
+
+
+@torch.library.custom_op("attnres_hip::sources_backward", mutates_args=(),
+                         device_types="cuda", tags=_OP_TAGS)
+def sources_backward(sources: list[Tensor], query: Tensor, out: Tensor, out_refine: Tensor,
+                     grad_out: Tensor, logit: Tensor, inv_rms: Tensor, stats: Tensor,
+                     scale: float) -> list[Tensor]:
+    return sources_backward_impl(sources, query, out, out_refine, grad_out, logit, inv_rms, stats, scale)
 
 
 @sources_backward.register_fake
@@ -383,15 +434,40 @@ def _sources_autograd(ctx: Any, grad_out, *_aux_grads):
 sources_forward.register_autograd(_sources_autograd, setup_context=_sources_setup_context)
 
 
+class _SourcesRead(torch.autograd.Function):
+    """The source-list read in eager mode (see ``_PackedRead``); the sources
+    come after the scalars so that each list position gets its gradient."""
+
+    @staticmethod
+    def forward(ctx, query: Tensor, eps: float, scale: float, *sources: Tensor):
+        outputs = sources_forward_impl(list(sources), query, eps, scale, saves_refinement(len(sources)))
+        _sources_setup_context(ctx, (sources, query, eps, scale), outputs)
+        return outputs
+
+    @staticmethod
+    def backward(ctx, grad_out, *_aux_grads):
+        count = ctx.count
+        if grad_out is None:
+            return (None, None, None, *([None] * count))
+        saved = ctx.saved_tensors
+        query, out, out_refine, logit, inv_rms, stats = saved[count:]
+        grads = sources_backward_impl(list(saved[:count]), query, out, out_refine, grad_out, logit, inv_rms,
+                                      stats, ctx.scale)
+        return (grads[count] if ctx.needs_input_grad[0] else None, None, None, *grads[:count])
+
+
 def sources_attnres(sources: tuple[Tensor, ...], query: Tensor, eps: float,
                     scale: float) -> Tensor:
     """Ordered source-list adapter (reference `fixed_tail_sources.source_attnres`,
     `fixed_tail_sources.py:186-195`): the list is passed through unpacked."""
-    return sources_forward(list(sources), _contiguous(query), eps, scale)[0]
+    query = _contiguous(query)
+    if _eager(query, *sources):
+        return _SourcesRead.apply(query, eps, scale, *sources)[0]
+    return sources_forward(list(sources), query, eps, scale)[0]
 
 
 __all__ = [
-    "RECOMPUTE_MAX_SOURCES", "packed_attnres", "packed_backward", "packed_forward", "packed_forward_impl",
-    "prepare_rows", "row_stride", "saves_refinement", "sources_attnres", "sources_backward", "sources_forward",
-    "sources_forward_impl",
+    "RECOMPUTE_MAX_SOURCES", "packed_attnres", "packed_backward", "packed_backward_impl", "packed_forward",
+    "packed_forward_impl", "prepare_rows", "row_stride", "saves_refinement", "sources_attnres", "sources_backward",
+    "sources_backward_impl", "sources_forward", "sources_forward_impl",
 ]
