@@ -243,3 +243,17 @@ def test_shared_sources_rejects_bad_inputs_on_the_host():
         SharedSources([torch.zeros(4, 8), torch.zeros(4, 8)])
     with pytest.raises(ValueError):
         SharedSources([torch.zeros(4, 8, dtype=torch.bfloat16), torch.zeros(4, 9, dtype=torch.bfloat16)])
+
+
+def test_eager_path_choice():
+    """Plain tensors and parameters take the direct autograd path; a compiler's
+    fake tensors take the registered ops (their fake kernels give the shapes)."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    from attnres import _ops
+
+    plain = torch.empty(3)
+    assert _ops._eager(plain, torch.nn.Parameter(torch.empty(2)))
+    with FakeTensorMode():
+        fake = torch.empty(3)
+    assert not _ops._eager(plain, fake)
