@@ -196,10 +196,25 @@ class _BankState:
         self.capacity = capacity
         self.gradients = gradients
         self._values: Tensor | None = None
+        self._flat: Tensor | None = None  # _values viewed as [capacity, tokens, width]
+        self._width = self._tokens = self._base = 0
+        self._device: torch.device | None = None
         self._grads: Tensor | None = None
         self._written: list[bool] = [False] * capacity
         self._pending: list[list[tuple[tuple, int]]] = [[] for _ in range(capacity)]
         self._pass = -1
+
+    def _allocate(self, source: Tensor) -> None:
+        self._values = torch.empty((self.capacity, *source.shape), device=source.device, dtype=torch.bfloat16)
+        self._width = int(source.shape[-1])
+        self._tokens = source.numel() // self._width
+        self._device = source.device
+        self._flat = self._values.view(self.capacity, self._tokens, self._width)
+        self._base = self._values.data_ptr()
+
+    def _slot_ptr(self, slot: int) -> int:
+        """Device address of slot ``slot``'s BF16 rows (the buffer is contiguous)."""
+        return self._base + slot * self._tokens * self._width * 2
 
     def _sources(self, slots: tuple[int, ...]) -> list[Tensor]:
         return [self._values[i] for i in slots]
@@ -221,10 +236,8 @@ class _BankState:
             return self._backward_coef(slots, query, out, out_refine, grad_out, logit, inv_rms, stats, scale)
         lib = _native.load()
         count = len(slots)
-        width = int(self._values.shape[-1])
-        tokens = self._values[0].numel() // width
+        width, tokens, device = self._width, self._tokens, self._device
         rank = query.numel()
-        device = self._values.device
         if self._grads is None:
             self._grads = torch.empty(self._values.shape, device=device, dtype=torch.float32)
         flags = (ctypes.c_uint8 * count)(*[1 if self._written[i] else 0 for i in slots])
@@ -240,7 +253,7 @@ class _BankState:
                     scale, *saved, self._grads.data_ptr(), grad_query.data_ptr(), workspace.data_ptr(),
                     workspace.numel(), flags, _stream(device))
             else:
-                pointers = (ctypes.c_void_p * count)(*[self._values[i].data_ptr() for i in slots])
+                pointers = (ctypes.c_void_p * count)(*[self._slot_ptr(i) for i in slots])
                 strides = (ctypes.c_int64 * count)(*([width] * count))
                 sums = (ctypes.c_void_p * count)(*[self._grads[i].data_ptr() for i in slots])
                 status = lib.attnres_hip_sources_backward_accumulate_f32(
@@ -257,10 +270,8 @@ class _BankState:
         the read's dO and coefficients are kept for the slots' gathers."""
         lib = _native.load()
         count = len(slots)
-        width = int(self._values.shape[-1])
-        tokens = self._values[0].numel() // width
+        width, tokens, device = self._width, self._tokens, self._device
         rank = query.numel()
-        device = self._values.device
         grad_query = torch.empty((rank,), device=device, dtype=torch.bfloat16)
         coef = torch.empty((3, count, tokens), device=device, dtype=torch.float32)
         workspace = _dq_workspace(lib, tokens, width, rank, device)
@@ -274,7 +285,7 @@ class _BankState:
                     scale, *saved, coef.data_ptr(), grad_query.data_ptr(), workspace.data_ptr(), workspace.numel(),
                     _stream(device))
             else:
-                pointers = (ctypes.c_void_p * count)(*[self._values[i].data_ptr() for i in slots])
+                pointers = (ctypes.c_void_p * count)(*[self._slot_ptr(i) for i in slots])
                 strides = (ctypes.c_int64 * count)(*([width] * count))
                 status = lib.attnres_hip_sources_backward_coef(
                     pointers, strides, count, tokens, width, query.data_ptr(), rank, scale, *saved, coef.data_ptr(),
@@ -307,8 +318,7 @@ class _BankState:
         if not pending:
             return None
         lib = _native.load()
-        width = int(self._values.shape[-1])
-        tokens = self._values[0].numel() // width
+        width, tokens, device = self._width, self._tokens, self._device
         reads = array("q")  # attnres_gather_read[len(pending)]
         for (_, head, rank), position in pending:
             reads.extend(head)
@@ -317,13 +327,12 @@ class _BankState:
         rank0 = pending[0][0][2]
         bf16 = (_BF16_GATHER and dtype == torch.bfloat16 and len(pending) <= _MAX_GATHER_READS
                 and all(rank == rank0 for (_, _, rank), _ in pending))
-        grad = torch.empty(self._values.shape[1:], device=self._values.device,
-                           dtype=torch.bfloat16 if bf16 else torch.float32)
-        with _on_device(self._values.device):
-            status = lib.attnres_hip_bank_gather(self._values[slot].data_ptr(), width, tokens, width,
+        grad = torch.empty(self._values.shape[1:], device=device, dtype=torch.bfloat16 if bf16 else torch.float32)
+        with _on_device(device):
+            status = lib.attnres_hip_bank_gather(self._slot_ptr(slot), width, tokens, width,
                                                  reads.buffer_info()[0], len(pending), grad.data_ptr(),
                                                  _DTYPE_BF16 if bf16 else _DTYPE_F32, 0,
-                                                 _stream(self._values.device))
+                                                 _stream(device))
         _native.check(status, "attnres source-bank gather")
         return grad
 
@@ -405,7 +414,7 @@ class SourceBank:
         if state._values is None:
             if source.ndim < 1 or source.numel() == 0 or not 1 <= source.shape[-1] <= _MAX_WIDTH:
                 raise ValueError("each source must have shape [...,D]")
-            state._values = torch.empty((self.capacity, *source.shape), device=source.device, dtype=torch.bfloat16)
+            state._allocate(source)
         elif source.shape != state._values.shape[1:] or source.device != state._values.device:
             raise ValueError("all source tensors must have the same logical shape and device")
         return slot
@@ -454,8 +463,8 @@ class SourceBank:
         if not slots:
             raise ValueError("a read needs at least one source")
         # the slots were checked at their push: BF16 rows [..., D] on one device
-        values = self._state._values
-        eps_value, scale_value = check_query(query, int(values.shape[-1]), values.device, eps, scale)
+        state = self._state
+        eps_value, scale_value = check_query(query, state._width, state._device, eps, scale)
         return _BankRead.apply(self._state, tuple(slots), query, eps_value, scale_value, self._token)
 
 
@@ -493,7 +502,7 @@ class _PushSum(torch.autograd.Function):
         dtype = _DTYPE_F32 if emitted.dtype == torch.float32 else _DTYPE_BF16
         with _on_device(emitted.device):
             status = lib.attnres_hip_partial_sum(prev.data_ptr(), emitted.data_ptr(), dtype, emitted.numel(),
-                                                 partial.data_ptr(), bank._values[slot].data_ptr(),
+                                                 partial.data_ptr(), bank._slot_ptr(slot),
                                                  _stream(emitted.device))
         _native.check(status, "attnres partial sum")
         ctx.bank, ctx.slot, ctx.dtype, ctx.token_device = bank, slot, emitted.dtype, emitted.device
@@ -516,7 +525,7 @@ class _BankRead(torch.autograd.Function):
         query = _contiguous(query)
         shape = bank._values.shape[1:]
         if bank._prefix(slots):
-            flat = bank._values[:len(slots)].reshape(len(slots), -1, shape[-1])  # a view: the bank is contiguous
+            flat = bank._flat[:len(slots)]
             out, out_refine, logit, inv_rms, stats = packed_forward_impl(flat, query, eps, scale, True, pooled=True)
         else:
             out, out_refine, logit, inv_rms, stats = sources_forward_impl(bank._sources(slots), query, eps, scale,
