@@ -80,8 +80,8 @@ CONFIGS = {
                name="block-schedule list S=9 N=32768 D=2048 R=2048, 3 reads sharing the sources"),
     "c5": dict(sources=48, batch=(16384,), widths=(1024, 4096),
                name="24-layer full-schedule sweep S=1..48 N=16384 D in {1024,4096} R in {D,D/4} packed"),
-    "policy": dict(sources=3, batch=(16384,), widths=(1024, 2048, 4096), rounds=5,
-                   name="save/recompute policy: reads of S=1..3 at N=16384, D in {1024,2048,4096}, R=D, packed"),
+    "policy": dict(sources=6, batch=(16384,), widths=(1024, 2048, 4096, 8192), rounds=5,
+                   name="save/recompute policy: reads of S=1..6 at N=16384, D in {1024,2048,4096,8192}, R=D, packed"),
     "model": dict(layers=24, width=1024, heads=16, ffn=2816, batch=16, sequence=1024, vocab=8192,
                   name="24-layer Full-schedule causal LM training step, D=1024, 16x1024 tokens, FP32 outside the reads"),
     "model_ref": dict(layers=24, width=1024, heads=16, ffn=2816, batch=2, sequence=1024, vocab=32768, autocast=True,
@@ -446,7 +446,7 @@ def run_sweep(cfg: dict, steps: int, warmup: int) -> dict:
 
 
 def run_policy(cfg: dict, steps: int, warmup: int) -> dict:
-    """policy: fwd+bwd of small reads (S <= 3) with the output refinement saved
+    """policy: fwd+bwd of small reads (S <= 6) with the output refinement saved
     (the streaming backward reads out + refinement) and without it (the
     recompute backward derives delta from the value rows); interleaved rounds,
     best round per variant.  The ops are called directly so the two variants
@@ -504,7 +504,7 @@ def run_policy(cfg: dict, steps: int, warmup: int) -> dict:
         torch.cuda.empty_cache()
     value = math.exp(sum(math.log(r) for r in ratios) / len(ratios))
     return {
-        "metric": "save/recompute policy: fwd+bwd time of reads with S<=3, saved-refinement path over recompute path "
+        "metric": "save/recompute policy: fwd+bwd time of reads with S<=6, saved-refinement path over recompute path "
                   "(geometric mean speedup)",
         "value": round(value, 4), "unit": "x", "n_gpus": 1, "steps": steps, "warmup": warmup,
         "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",

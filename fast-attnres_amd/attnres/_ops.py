@@ -36,7 +36,9 @@ anyway.  The reference makes the same structural choice
 (`fla_full_sources._should_save_mixed`, `fla_full_sources.py:146-161`:
 recompute for S <= 3) but saves an FP32 copy of the output for larger reads
 (`fixed_tail.py:917-919`): four extra bytes per element written in the
-forward and read in the backward instead of one.
+forward and read in the backward instead of one.  Here the threshold is 6:
+the recompute backward holds a token's rows in registers, and up to six
+rows that is faster than writing and re-reading the refinement.
 """
 
 from __future__ import annotations
@@ -55,7 +57,7 @@ _F32 = torch.float32
 _BF16 = torch.bfloat16
 
 # Save/recompute policy (attnres_hip.h ATTNRES_RECOMPUTE_MAX_SOURCES).
-RECOMPUTE_MAX_SOURCES = 3
+RECOMPUTE_MAX_SOURCES = 6
 
 
 def saves_refinement(sources: int) -> bool:

@@ -40,7 +40,7 @@
 // per group, or two for aligned 4-chunk rows where that does not spill (see
 // launch_bwd).
 //
-// Variants of the backward.  For S <= 3 (the save/recompute policy) a group
+// Variants of the backward.  For S <= 6 (the save/recompute policy) a group
 // holds all S rows of its token and takes delta = sum_s p_s dw_s from them,
 // so the forward stores no refinement and the backward reads no saved output
 // (attnres_bwd_recompute_kernel).  The accumulating variant adds dv to
@@ -917,10 +917,10 @@ __global__ void __launch_bounds__(kBlock) attnres_bwd_kernel(const BwdArgs<Rows,
 // comes from the dw_s = <v_s, dO> it needs anyway (o = sum_s p_s v_s),
 // summed in source order.  Grid-stride over tokens on the persistent grid;
 // the S + 1 rows of a token are requested together and occupancy hides
-// their latency.  Rows s >= S re-read row 0 (cached) and are not used.
-template <int G, int CH, bool NOMASK, bool VEC, class Rows, class Grads>
+// their latency.  SM (>= S) rows are held; rows s >= S re-read row 0
+// (cached) and are not used, so reads of few sources take a small SM.
+template <int G, int CH, int SM, bool NOMASK, bool VEC, class Rows, class Grads>
 __global__ void __launch_bounds__(kBlock) attnres_bwd_recompute_kernel(const BwdArgs<Rows, Grads> a) {
-  constexpr int SM = kRecomputeMaxSources;
   static_assert(G <= 64 || G == kBlock, "a wide group is the whole workgroup");
   constexpr int kGroups = kBlock / G;
   __shared__ float xred[xred_floats<G>(SM)];
@@ -1290,13 +1290,22 @@ int64_t launch_bwd_geometry(const BwdArgs<Rows, Grads>& a, bool nomask, bool vec
              : launch_bwd_variant<G, CH, false>(a, nomask, vec, stream);
 }
 
-template <int G, int CH, bool NOMASK, bool VEC, class Rows, class Grads>
-int64_t launch_bwd_recompute(const BwdArgs<Rows, Grads>& a, hipStream_t stream) {
-  const int64_t resident = resident_blocks<&attnres_bwd_recompute_kernel<G, CH, NOMASK, VEC, Rows, Grads>>();
+template <int G, int CH, int SM, bool NOMASK, bool VEC, class Rows, class Grads>
+int64_t launch_bwd_recompute_rows(const BwdArgs<Rows, Grads>& a, hipStream_t stream) {
+  const int64_t resident = resident_blocks<&attnres_bwd_recompute_kernel<G, CH, SM, NOMASK, VEC, Rows, Grads>>();
   const int64_t blocks = grid_blocks(a.n_tokens, a.width, resident);
-  hipLaunchKernelGGL((attnres_bwd_recompute_kernel<G, CH, NOMASK, VEC, Rows, Grads>),
+  hipLaunchKernelGGL((attnres_bwd_recompute_kernel<G, CH, SM, NOMASK, VEC, Rows, Grads>),
                      dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream, a);
   return blocks;
+}
+
+// Rows held per lane: 3 for reads of at most 3 sources, else the policy's
+// maximum.
+template <int G, int CH, bool NOMASK, bool VEC, class Rows, class Grads>
+int64_t launch_bwd_recompute(const BwdArgs<Rows, Grads>& a, hipStream_t stream) {
+  constexpr int kFew = kRecomputeMaxSources < 3 ? kRecomputeMaxSources : 3;
+  if (a.n_sources <= kFew) return launch_bwd_recompute_rows<G, CH, kFew, NOMASK, VEC>(a, stream);
+  return launch_bwd_recompute_rows<G, CH, kRecomputeMaxSources, NOMASK, VEC>(a, stream);
 }
 
 // The recompute kernel keeps S rows per lane: for the (64, 8) geometry

@@ -41,8 +41,10 @@
  * the forward (nothing is stored) and out = out_refine = NULL to the plain
  * backward, which then derives delta = <dO, o> = sum_s p_s <v_s, dO> from
  * the value rows it reads anyway.  Larger reads must save it.  (The reference
- * makes the same structural choice: recompute for S <= 3, save the FP32
- * mixed output for S >= 4, src/attnres/_kernels/fla_full_sources.py:146-161.)
+ * makes the same structural choice with a threshold of 3: recompute for
+ * S <= 3, save the FP32 mixed output for S >= 4,
+ * src/attnres/_kernels/fla_full_sources.py:146-161.  Here the recompute
+ * backward holds a token's rows in registers, which pays up to 6 sources.)
  */
 #ifndef ATTNRES_HIP_H
 #define ATTNRES_HIP_H
@@ -67,7 +69,7 @@ enum attnres_status {
 #define ATTNRES_MAX_SOURCES 129
 #define ATTNRES_MAX_WIDTH 8192
 /* Reads of at most this many sources may skip the refinement (see above). */
-#define ATTNRES_RECOMPUTE_MAX_SOURCES 3
+#define ATTNRES_RECOMPUTE_MAX_SOURCES 6
 
 /* Element types of attnres_hip_partial_sum and attnres_hip_bank_gather. */
 #define ATTNRES_DTYPE_F32 0

@@ -123,5 +123,5 @@ def test_random_source_bank_stream_matches_attnres(index):
             continue
         scale = float(b.float().abs().max()) or 1.0
         # source gradients: FP32 sums vs autograd's sums of per-read BF16 dv; dq: the saved and the
-        # recompute backward (attnres takes the recompute kernel for reads of at most 3 sources)
+        # recompute backward (attnres takes the recompute kernel for reads of at most 6 sources)
         torch.testing.assert_close(a.float(), b.float(), rtol=2.0**-6, atol=2.0**-6 * scale)

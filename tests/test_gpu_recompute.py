@@ -1,4 +1,4 @@
-"""The save/recompute policy on the GPU: reads of at most 3 sources store no
+"""The save/recompute policy on the GPU: reads of at most 6 sources store no
 output refinement, and their backward (`attnres_bwd_recompute_kernel`) gets
 delta = <dO, o> = sum_s p_s <v_s, dO> from the value rows.
 
@@ -7,8 +7,9 @@ lanes, one or several chunks per lane, a whole workgroup per token above
 D = 2048), with and without key masks, on the vectorised (aligned) and the
 element-wise (padded rows) path, packed and as a source list; and against
 the saved-refinement backward on the same inputs, which computes the same
-gradients from the saved output instead (reference policy: recompute for
-S <= 3, `src/attnres/_kernels/fla_full_sources.py:146-161`).
+gradients from the saved output instead (the reference recomputes for
+S <= 3, `src/attnres/_kernels/fla_full_sources.py:146-161`; the register-resident
+backward pays up to S = 6 here).
 """
 
 from __future__ import annotations
@@ -43,7 +44,7 @@ def _inputs(sources, tokens, width, rank, padded, seed):
 @pytest.mark.parametrize("layout", ["packed", "list"])
 @pytest.mark.parametrize("padded", [False, True], ids=["aligned", "padded"])
 @pytest.mark.parametrize("width,rank", WIDTHS, ids=lambda v: str(v))
-@pytest.mark.parametrize("sources", [1, 2, 3])
+@pytest.mark.parametrize("sources", [1, 2, 3, 4, 6])
 def test_recompute_backward_matches_oracle(sources, width, rank, padded, layout):
     tokens = 37
     producer, query, upstream = _inputs(sources, tokens, width, rank, padded, SEEDS[0] + width + sources)
@@ -64,7 +65,7 @@ def test_recompute_backward_matches_oracle(sources, width, rank, padded, layout)
 @pytest.mark.parametrize("layout", ["packed", "list"])
 @pytest.mark.parametrize("width,rank", [(1000, 96), (2048, 2048), (4096, 1024), (8192, 8192)],
                          ids=lambda v: str(v))
-@pytest.mark.parametrize("sources", [2, 3])
+@pytest.mark.parametrize("sources", [2, 3, 5, 6])
 def test_recompute_agrees_with_the_saved_refinement_path(sources, width, rank, layout):
     """Same inputs through both backward kernels: the forward output is the
     same bits, dv agrees to BF16 rounding and dq to FP32 rounding of delta."""

@@ -151,35 +151,36 @@ def test_accumulating_backward_needs_its_flags_and_checks_like_the_plain_one():
 
 def test_save_recompute_policy_matches_the_header_and_the_ops():
     """Reads of at most ATTNRES_RECOMPUTE_MAX_SOURCES sources save no
-    refinement (reference fla_full_sources.py:146-161: recompute for S <= 3)."""
+    refinement (the reference recomputes for S <= 3, fla_full_sources.py:146-161;
+    the register-resident backward pays up to 6 here)."""
     from attnres import _ops
 
     lib = _native.load()
     text = HEADER.read_text()
     assert f"#define ATTNRES_RECOMPUTE_MAX_SOURCES {_ops.RECOMPUTE_MAX_SOURCES}" in text
-    assert _ops.RECOMPUTE_MAX_SOURCES == 3
+    assert _ops.RECOMPUTE_MAX_SOURCES == 6
     for count in range(1, 130):
-        assert bool(lib.attnres_hip_saves_refinement(count)) == _ops.saves_refinement(count) == (count > 3)
+        assert bool(lib.attnres_hip_saves_refinement(count)) == _ops.saves_refinement(count) == (count > 6)
 
 
 def test_backward_without_the_refinement_is_for_small_reads_only():
-    """out_refine = NULL selects the recompute kernel: more than 3 sources is a
+    """out_refine = NULL selects the recompute kernel: more than 6 sources is a
     shape error, and the accumulating entry points still need the refinement;
     both are rejected on the host."""
     lib = _native.load()
     need = lib.attnres_hip_dq_workspace_elems(4, 64, 16)
     stats = (_FAKE, _FAKE, _FAKE)
     status = lib.attnres_hip_packed_backward(
-        _FAKE, 64, 64, 4, 4, 64, _FAKE, 16, 1.0, None, None, _FAKE, *stats, _FAKE, _FAKE, _FAKE, need, None)
+        _FAKE, 64, 64, 7, 4, 64, _FAKE, 16, 1.0, None, None, _FAKE, *stats, _FAKE, _FAKE, _FAKE, need, None)
     assert status == _native.ERR_SHAPE
-    assert b"n_sources <= 3" in lib.attnres_hip_last_error()
+    assert b"n_sources <= 6" in lib.attnres_hip_last_error()
     status = lib.attnres_hip_packed_backward(  # small read: checks pass up to the workspace
-        _FAKE, 64, 64, 3, 4, 64, _FAKE, 16, 1.0, None, None, _FAKE, *stats, _FAKE, _FAKE, _FAKE, need - 1, None)
+        _FAKE, 64, 64, 6, 4, 64, _FAKE, 16, 1.0, None, None, _FAKE, *stats, _FAKE, _FAKE, _FAKE, need - 1, None)
     assert status == _native.ERR_WORKSPACE
-    pointers = (ctypes.c_void_p * 4)(_FAKE, _FAKE, _FAKE, _FAKE)
-    strides = (ctypes.c_int64 * 4)(64, 64, 64, 64)
+    pointers = (ctypes.c_void_p * 7)(*[_FAKE] * 7)
+    strides = (ctypes.c_int64 * 7)(*[64] * 7)
     status = lib.attnres_hip_sources_backward(
-        pointers, strides, 4, 4, 64, _FAKE, 16, 1.0, None, None, _FAKE, *stats, pointers, _FAKE, _FAKE, need, None)
+        pointers, strides, 7, 4, 64, _FAKE, 16, 1.0, None, None, _FAKE, *stats, pointers, _FAKE, _FAKE, need, None)
     assert status == _native.ERR_SHAPE
     flags = (ctypes.c_uint8 * 3)(0, 0, 0)
     status = lib.attnres_hip_packed_backward_accumulate(
