@@ -321,11 +321,8 @@ int check_recompute(bool recompute, int64_t S, const char* name) {
   return ATTNRES_OK;
 }
 
-// Workspace layout (FP32): [max_blocks, R] partial rows, [R] total.
-int64_t workspace_elems(int64_t N, int64_t D, int64_t R) {
-  const int64_t rows = grid_blocks(N, D, 0);
-  return (rows + 1) * R;
-}
+// Workspace layout (FP32): [max_grid_rows, R] partial rows, [R] total.
+int64_t workspace_elems(int64_t N, int64_t D, int64_t R) { return (max_grid_rows(N, D) + 1) * R; }
 
 }  // namespace
 }  // namespace attnres_hip
@@ -424,6 +421,7 @@ int packed_backward(const void* values, int64_t source_stride, int64_t row_strid
   a.inv_rms = inv_rms;
   a.stats = stats;
   a.partial = dq_workspace;
+  a.max_grid = need / rank - 1;
   a.n_tokens = n_tokens;
   a.n_sources = static_cast<int>(n_sources);
   a.width = static_cast<int>(width);
@@ -568,6 +566,7 @@ int sources_backward(const void* const* sources, const int64_t* row_strides, int
   a.inv_rms = inv_rms;
   a.stats = stats;
   a.partial = dq_workspace;
+  a.max_grid = need / rank - 1;
   a.n_tokens = n_tokens;
   a.n_sources = static_cast<int>(n_sources);
   a.width = static_cast<int>(width);

@@ -127,6 +127,8 @@ struct BwdArgs {
   const float* inv_rms;
   const float* stats;
   float* partial;            // [gridDim.x, R] FP32 dq partial rows
+  int64_t max_grid;          // host side only: the launch may not exceed this many workgroups
+                             // (the partial rows `partial` holds); the kernels ignore it
   int64_t n_tokens;
   int n_sources;
   int width;
@@ -194,13 +196,31 @@ inline bool no_mask(const Geometry& geo, int64_t width, int64_t rank) {
   return rank == width && width == static_cast<int64_t>(geo.lanes) * geo.chunks * kVec;
 }
 
-// Persistent grid: one group per token at most, capped by the workgroups that
-// stay resident on the device (`resident` <= 0: unknown) and kMaxGridBlocks.
-inline int64_t grid_blocks(int64_t N, int64_t D, int64_t resident) {
-  const int64_t groups = kBlock / geometry(D).lanes;
+// Lanes per token group of the recompute backward: it keeps S rows per lane,
+// so for the (64, 8) geometry (2048 < D <= 4096) it runs a whole workgroup
+// per token with 2 chunks per lane; every other geometry keeps its group.
+constexpr int recompute_lanes(int lanes, int chunks) { return lanes == 64 && chunks == 8 ? kBlock : lanes; }
+
+// Persistent grid for N tokens in groups of `group_lanes` lanes: one group
+// per token at most, capped by the workgroups that stay resident on the
+// device (`resident` <= 0: unknown), by kMaxGridBlocks and by `cap` (<= 0:
+// none; the dq partial rows the caller's buffer holds).
+inline int64_t grid_blocks(int64_t N, int group_lanes, int64_t resident, int64_t cap = 0) {
+  const int64_t groups = kBlock / group_lanes;
   int64_t blocks = (N + groups - 1) / groups;
   if (resident > 0 && blocks > resident) blocks = resident;
+  if (cap > 0 && blocks > cap) blocks = cap;
   return blocks < kMaxGridBlocks ? blocks : kMaxGridBlocks;
+}
+
+// The most workgroups any backward variant launches for N tokens of width D
+// (the streaming kernel with the geometry's groups, the recompute kernel with
+// recompute_lanes), i.e. the dq partial rows a workspace must hold.
+inline int64_t max_grid_rows(int64_t N, int64_t D) {
+  const Geometry geo = geometry(D);
+  const int lanes = recompute_lanes(geo.lanes, geo.chunks) > geo.lanes ? recompute_lanes(geo.lanes, geo.chunks)
+                                                                        : geo.lanes;
+  return grid_blocks(N, lanes, 0);
 }
 
 // ----------------------------------------------------------------- launchers

@@ -1239,8 +1239,7 @@ void launch_fwd(const FwdArgs<Rows>& a, hipStream_t stream) {
   constexpr int64_t kGroups = kBlock / G;
   int64_t blocks = (a.n_tokens + kGroups - 1) / kGroups;
   if (a.n_sources <= kPersistentFwdMaxSources) {
-    blocks = grid_blocks(a.n_tokens, a.width,
-                         resident_blocks<&attnres_fwd_kernel<G, CH, fwd_ring<CH>(), NOMASK, VEC, Rows>>());
+    blocks = grid_blocks(a.n_tokens, G, resident_blocks<&attnres_fwd_kernel<G, CH, fwd_ring<CH>(), NOMASK, VEC, Rows>>());
   }
   hipLaunchKernelGGL((attnres_fwd_kernel<G, CH, fwd_ring<CH>(), NOMASK, VEC, Rows>),
                      dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream, a);
@@ -1260,7 +1259,7 @@ void launch_fwd_geometry(const FwdArgs<Rows>& a, bool nomask, bool vec, hipStrea
 template <int G, int CH, int NB, bool NOMASK, bool VEC, bool ACC, class Rows, class Grads>
 int64_t launch_bwd_ring(const BwdArgs<Rows, Grads>& a, hipStream_t stream) {
   const int64_t resident = resident_blocks<&attnres_bwd_kernel<G, CH, NB, NOMASK, VEC, ACC, Rows, Grads>>();
-  const int64_t blocks = grid_blocks(a.n_tokens, a.width, resident);
+  const int64_t blocks = grid_blocks(a.n_tokens, G, resident, a.max_grid);
   hipLaunchKernelGGL((attnres_bwd_kernel<G, CH, NB, NOMASK, VEC, ACC, Rows, Grads>),
                      dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream, a);
   return blocks;
@@ -1293,7 +1292,7 @@ int64_t launch_bwd_geometry(const BwdArgs<Rows, Grads>& a, bool nomask, bool vec
 template <int G, int CH, int SM, bool NOMASK, bool VEC, class Rows, class Grads>
 int64_t launch_bwd_recompute_rows(const BwdArgs<Rows, Grads>& a, hipStream_t stream) {
   const int64_t resident = resident_blocks<&attnres_bwd_recompute_kernel<G, CH, SM, NOMASK, VEC, Rows, Grads>>();
-  const int64_t blocks = grid_blocks(a.n_tokens, a.width, resident);
+  const int64_t blocks = grid_blocks(a.n_tokens, G, resident, a.max_grid);
   hipLaunchKernelGGL((attnres_bwd_recompute_kernel<G, CH, SM, NOMASK, VEC, Rows, Grads>),
                      dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream, a);
   return blocks;
@@ -1310,12 +1309,12 @@ int64_t launch_bwd_recompute(const BwdArgs<Rows, Grads>& a, hipStream_t stream) 
 
 // The recompute kernel keeps S rows per lane: for the (64, 8) geometry
 // (2048 < D <= 4096) it runs with a whole workgroup per token instead, two
-// chunks per lane (same lane positions covered, so the same NOMASK rule).
+// chunks per lane (same lane positions covered, so the same NOMASK rule);
+// its grid counts those groups (one token per workgroup).
 template <int G, int CH, class Rows, class Grads>
 int64_t launch_bwd_recompute_geometry(const BwdArgs<Rows, Grads>& a, bool nomask, bool vec, hipStream_t stream) {
-  constexpr bool kWide = G == 64 && CH == 8;
-  constexpr int RG = kWide ? kBlock : G;
-  constexpr int RCH = kWide ? 2 : CH;
+  constexpr int RG = recompute_lanes(G, CH);
+  constexpr int RCH = G * CH / RG;
   static_assert(RG * RCH == G * CH, "same row coverage");
   if (nomask) {
     return vec ? launch_bwd_recompute<RG, RCH, true, true>(a, stream)
@@ -1337,8 +1336,10 @@ int64_t launch_bwd_geometry_coef(const BwdArgs<Rows, CoefSink>& a, bool nomask, 
 
 template <int G, int CH, bool VEC, bool BF16OUT, int RING>
 void launch_gather_ring(const GatherArgs& a, hipStream_t stream) {
-  const int64_t blocks =
-      grid_blocks(a.n_tokens, a.width, resident_blocks<&attnres_gather_kernel<G, CH, VEC, BF16OUT, RING>>());
+  // the grid of the row geometry's token groups (the gather's own groups are
+  // wider: it has no group sums and spreads a row over up to a workgroup)
+  const int64_t blocks = grid_blocks(a.n_tokens, geometry(a.width).lanes,
+                                     resident_blocks<&attnres_gather_kernel<G, CH, VEC, BF16OUT, RING>>());
   hipLaunchKernelGGL((attnres_gather_kernel<G, CH, VEC, BF16OUT, RING>), dim3(static_cast<unsigned>(blocks)),
                      dim3(kBlock), 0, stream, a);
 }

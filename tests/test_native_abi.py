@@ -281,3 +281,15 @@ def test_coefficient_backward_and_gather_check_on_the_host():
     many = (_GatherRead * 49)(*[(_FAKE, _FAKE, _FAKE, 3, 0, 16)] * 49)
     assert lib.attnres_hip_bank_gather(_FAKE, 64, 4, 64, many, 49, _FAKE, bf16, 0, None) == _native.ERR_SHAPE
     assert b"at most 48 reads" in lib.attnres_hip_last_error()
+
+
+def test_workspace_holds_the_widest_backward_grid():
+    """The dq workspace holds one partial row per workgroup of the widest
+    backward variant plus the total: for 2048 < D <= 4096 the recompute kernel
+    runs one token per workgroup, elsewhere the geometry's groups share one."""
+    lib = _native.load()
+    assert lib.attnres_hip_dq_workspace_elems(100, 3000, 257) == (100 + 1) * 257
+    assert lib.attnres_hip_dq_workspace_elems(100, 2048, 2048) == (25 + 1) * 2048    # 4 groups of 64 lanes
+    assert lib.attnres_hip_dq_workspace_elems(100, 1024, 1024) == (13 + 1) * 1024    # 8 groups of 32 lanes
+    assert lib.attnres_hip_dq_workspace_elems(100, 8192, 8192) == (100 + 1) * 8192   # a workgroup per token
+    assert lib.attnres_hip_dq_workspace_elems(10**6, 4096, 64) == (2048 + 1) * 64    # the persistent-grid cap
