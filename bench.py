@@ -72,6 +72,8 @@ HBM_PEAK_TBS = 8.0  # MI355X HBM3E peak, TB/s
 
 # name -> (sources, tokens as (batch, seq), width, rank)
 CONFIGS = {
+    "c1": dict(sources=8, batch=(2, 512), width=1024, rank=1024, outliers=False, input_device="cpu",
+               name="cpu-plumbing-read S=8 N=1024 D=1024 R=1024 packed (CPU FP32 oracle config)"),
     "c2": dict(sources=25, batch=(8, 2048), width=2048, rank=2048,
                name="standard-full-read S=25 N=16384 D=2048 R=2048 packed"),
     "c3": dict(sources=16, batch=(16384,), width=4096, rank=1024,
@@ -101,22 +103,49 @@ def read_bytes(sources: int, tokens: int, width: int) -> tuple[int, int]:
 
 
 def make_inputs(cfg: dict, device, seed: int = 0):
+    """Packed BASELINE inputs: values ``[S, *batch, D]`` with per-source std
+    U[0.5, 4] and (unless ``outliers`` is False, as in c1) 1% of channels x8,
+    query N(0,1)/sqrt(R), dO N(0,1); seeded ``torch.Generator`` draws on
+    ``input_device`` (default: ``device``), then moved to ``device``."""
     import torch
 
+    target = torch.device(device)
+    device = torch.device(cfg.get("input_device", target))
     generator = torch.Generator(device=device).manual_seed(seed)
     sources, width, rank = cfg["sources"], cfg["width"], cfg["rank"]
     shape = (sources, *cfg["batch"], width)
     std = torch.rand(sources, generator=generator, device=device) * 3.5 + 0.5
     channel_scale = torch.ones(width, device=device)
-    outliers = torch.randperm(width, generator=generator, device=device)[: max(1, width // 100)]
-    channel_scale[outliers] = 8.0
+    if cfg.get("outliers", True):
+        outliers = torch.randperm(width, generator=generator, device=device)[: max(1, width // 100)]
+        channel_scale[outliers] = 8.0
     values = torch.empty(shape, device=device, dtype=torch.bfloat16)
     for s in range(sources):  # per source keeps the FP32 temporary small
         noise = torch.randn(shape[1:], generator=generator, device=device)
         values[s] = (noise * std[s] * channel_scale).to(torch.bfloat16)
     query = (torch.randn(rank, generator=generator, device=device) / math.sqrt(rank)).to(torch.bfloat16)
     grad_out = torch.randn(shape[1:], generator=generator, device=device).to(torch.bfloat16)
-    return values, query, grad_out
+    return values.to(target), query.to(target), grad_out.to(target)
+
+
+def make_block_sources(cfg: dict, device, seed: int = 0):
+    """c4 inputs: ``sources`` separately allocated BF16 ``[N, D]`` tensors (source
+    0 the embedding, std 1; the rest block sums, std sqrt(3)*U[0.5, 2]), one
+    query ``[R]`` N(0,1)/sqrt(R) and one dO ``[N, D]`` per read."""
+    import torch
+
+    generator = torch.Generator(device=device).manual_seed(seed)
+    tokens, width, rank, reads = cfg["batch"][0], cfg["width"], cfg["rank"], cfg["reads"]
+    sources = []
+    for s in range(cfg["sources"]):
+        std = 1.0 if s == 0 else math.sqrt(3.0) * (0.5 + 1.5 * float(torch.rand((), generator=generator, device=device)))
+        noise = torch.randn(tokens, width, generator=generator, device=device)
+        sources.append((noise * std).to(torch.bfloat16))
+    queries = [(torch.randn(rank, generator=generator, device=device) / math.sqrt(rank)).to(torch.bfloat16)
+               for _ in range(reads)]
+    grad_outs = [torch.randn(tokens, width, generator=generator, device=device).to(torch.bfloat16)
+                 for _ in range(reads)]
+    return sources, queries, grad_outs
 
 
 def measured_traffic(config: str, key: str) -> int | None:
@@ -144,28 +173,58 @@ def copy_probe(gib: float = 1.0, reps: int = 5) -> None:
                       "reps": reps}), flush=True)
 
 
-def cpu_baseline(values, query, grad_out, budget_s: float, chunk: int) -> dict:
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _cpu_threads() -> tuple[int, int]:
+    """(threads used, CPUs visible).  The threads are the job's CPU share:
+    OMP_NUM_THREADS when the host sets it (16 per GPU on the MI355X boxes,
+    whose affinity mask shows the whole machine), else every visible CPU."""
+    visible = len(os.sched_getaffinity(0))
+    share = int(os.environ.get("OMP_NUM_THREADS") or visible)
+    return max(1, min(visible, share)), visible
+
+
+def cpu_baseline(values, query, grad_out, budget_s: float, chunk: int, reads: int = 1) -> dict:
     """Time the CPU FP32 oracle (forward + backward) over token chunks of the
     same inputs until ``budget_s`` seconds of oracle time have been spent;
-    scale to one full read.  Tokens are independent, so chunking changes no
-    result (dq is a sum over tokens)."""
+    scale to one full read (``reads`` reads for a step of several).  Tokens are
+    independent, so chunking changes no result (dq is a sum over tokens).
+    ``values``: packed ``[S, ..., D]`` or a list of ``[N, D]`` sources."""
     import torch
 
     from oracle.oracle import oracle_with_grads
 
-    cores = min(16, len(os.sched_getaffinity(0)))
+    cores, visible = _cpu_threads()
     torch.set_num_threads(cores)
-    sources, width = values.shape[0], values.shape[-1]
-    flat = values.reshape(sources, -1, width)
+    listed = isinstance(values, (list, tuple))
+    width = int(values[0].shape[-1])
+    if listed:
+        flat = [v.reshape(-1, width) for v in values]
+        sources, tokens = len(flat), int(flat[0].shape[0])
+    else:
+        sources = int(values.shape[0])
+        flat = values.reshape(sources, -1, width)
+        tokens = int(flat.shape[1])
     upstream = grad_out.reshape(-1, width)
-    tokens = flat.shape[1]
     query_cpu = query.cpu()
+
+    def rows(start, stop):
+        return [v[start:stop].cpu() for v in flat] if listed else flat[:, start:stop].cpu()
+
     # one untimed warm-up chunk (thread pool, allocator)
-    oracle_with_grads(flat[:, :256].cpu(), query_cpu, upstream[:256].cpu())
+    oracle_with_grads(rows(0, min(tokens, 256)), query_cpu, upstream[:256].cpu())
     done, spent = 0, 0.0
     while done < tokens and spent < budget_s:
         stop = min(tokens, done + chunk)
-        v, g = flat[:, done:stop].cpu(), upstream[done:stop].cpu()
+        v, g = rows(done, stop), upstream[done:stop].cpu()
         start = time.perf_counter()
         oracle_with_grads(v, query_cpu, g)
         spent += time.perf_counter() - start
@@ -176,11 +235,15 @@ def cpu_baseline(values, query, grad_out, budget_s: float, chunk: int) -> dict:
         "value": round((fwd + bwd) / seconds_per_read / 1e12, 6),
         "unit": "TB/s",
         "us_per_read": round(seconds_per_read * 1e6, 1),
+        "us_per_step": round(seconds_per_read * reads * 1e6, 1),
         "cores": cores,
+        "host_cpus_visible": visible,
+        "cpu_model": _cpu_model(),
         "kind": "port",
-        "sample": (f"CPU FP32 eager oracle (oracle/oracle.py, torch {torch.__version__}), "
-                   f"forward+backward over {done} of {tokens} tokens of the same inputs in "
-                   f"chunks of {chunk}, {spent:.1f} s, scaled to one full read"),
+        "sample": (f"CPU FP32 eager oracle (oracle/oracle.py, torch {torch.__version__}, {cores} threads), "
+                   f"forward+backward over {done} of {tokens} tokens of the same inputs"
+                   f"{' (one read of the step)' if reads > 1 else ''} in chunks of {chunk}, {spent:.1f} s, "
+                   f"scaled to one full read"),
     }
 
 
@@ -212,7 +275,8 @@ def graph_replay(values, query, grad_out, cfg: dict, replays: int = 20, rounds: 
     N = packed.shape[1]
     dev = packed.device
     out = torch.empty(N, width, device=dev, dtype=torch.bfloat16)
-    refine = torch.empty(N if S > 3 else 0, width, device=dev, dtype=torch.int8)
+    # the product path's save/recompute policy: no refinement for small reads
+    refine = torch.empty(N if lib.attnres_hip_saves_refinement(S) else 0, width, device=dev, dtype=torch.int8)
     logit, inv_rms = torch.empty(N, S, device=dev), torch.empty(N, S, device=dev)
     stats = torch.empty(2, N, device=dev)
     dv = torch.empty_like(packed)
@@ -280,7 +344,7 @@ def _event():
     return torch.cuda.Event(enable_timing=True)
 
 
-def run_block_schedule(cfg: dict, steps: int, warmup: int) -> dict:
+def run_block_schedule(cfg: dict, steps: int, warmup: int, cpu_budget: float | None = None) -> dict:
     """c4: 3 reads of one ordered list of 9 sources, each read with its own
     query; per read forward, then per read backward (so the operator time
     excludes the gradient accumulation over the shared sources, which is
@@ -290,16 +354,10 @@ def run_block_schedule(cfg: dict, steps: int, warmup: int) -> dict:
     from attnres import attnres
 
     device = torch.device("cuda:0")
-    generator = torch.Generator(device=device).manual_seed(0)
     tokens, width, rank, reads = cfg["batch"][0], cfg["width"], cfg["rank"], cfg["reads"]
-    sources = []
-    for s in range(cfg["sources"]):  # source 0: embedding (std 1); then block sums
-        std = 1.0 if s == 0 else math.sqrt(3.0) * (0.5 + 1.5 * float(torch.rand((), generator=generator, device=device)))
-        noise = torch.randn(tokens, width, generator=generator, device=device)
-        sources.append((noise * std).to(torch.bfloat16).requires_grad_())
-    queries = [(torch.randn(rank, generator=generator, device=device) / math.sqrt(rank)).to(torch.bfloat16).requires_grad_()
-               for _ in range(reads)]
-    grad_outs = [torch.randn(tokens, width, generator=generator, device=device).to(torch.bfloat16) for _ in range(reads)]
+    sources, queries, grad_outs = make_block_sources(cfg, device, seed=0)
+    sources = [source.requires_grad_() for source in sources]
+    queries = [query.requires_grad_() for query in queries]
     listed = tuple(sources)
 
     def step(ev=None):
@@ -381,7 +439,9 @@ def run_block_schedule(cfg: dict, steps: int, warmup: int) -> dict:
         "roofline": {"bound": "hbm", "kernel": "backward op (list layout)", "achieved": round(bwd_tbs * 1e3, 1),
                      "peak": HBM_PEAK_TBS * 1e3, "unit": "GB/s", "frac": round(bwd_tbs / HBM_PEAK_TBS, 4),
                      "traffic": measured_traffic("c4", "backward_bytes")},
-        "cpu_baseline": None,
+        "cpu_baseline": (None if cpu_budget is None else
+                         cpu_baseline([s.detach() for s in listed], queries[0].detach(), grad_outs[0], cpu_budget,
+                                      chunk=2048, reads=reads)),
     }
 
 
@@ -679,7 +739,10 @@ def main(argv=None) -> int:
             result = run_model(cfg, args.steps, args.warmup, args.model_variant, args.autocast == "bf16")
         else:
             run = {"c4": run_block_schedule, "c5": run_sweep, "policy": run_policy}[args.config]
-            result = run(cfg, args.steps, args.warmup)
+            if args.config == "c4":
+                result = run(cfg, args.steps, args.warmup, None if args.no_cpu_baseline else args.cpu_budget)
+            else:
+                result = run(cfg, args.steps, args.warmup)
         print(json.dumps(result), flush=True)
         return 0
     device = torch.device("cuda:0")
@@ -742,7 +805,8 @@ def main(argv=None) -> int:
         "vs_baseline": None,
         "dtype": "f32",
         "storage_dtype": "bf16",
-        "data": "synthetic (seeded; per-source std U[0.5,4], 1% channels x8)",
+        "data": ("synthetic (seeded; per-source std U[0.5,4]"
+                 + (", 1% channels x8)" if cfg.get("outliers", True) else "; drawn on the CPU)")),
         "config": {"workload": cfg["name"], "sources": sources, "tokens": tokens,
                    "width": width, "rank": cfg["rank"], "layout": "packed",
                    "bytes_per_read": fwd_bytes + bwd_bytes},

@@ -29,3 +29,18 @@ def _gpu_required(request):
         assert torch.cuda.is_available(), "gpu test selected but no ROCm GPU is visible"
         torch.compiler.reset()
     yield
+
+
+def pytest_sessionfinish(session, exitstatus):
+    """With ATTNRES_PARITY_TABLE=<path>, write the recorded error metrics of
+    every comparison (tests/helpers.py) as JSON."""
+    import json
+    import os
+
+    path = os.environ.get("ATTNRES_PARITY_TABLE")
+    if not path:
+        return
+    helpers = sys.modules.get("helpers")
+    records = getattr(helpers, "RECORDS", []) if helpers else []
+    Path(path).parent.mkdir(parents=True, exist_ok=True)
+    Path(path).write_text(json.dumps(records, indent=1))

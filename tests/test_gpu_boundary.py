@@ -1,0 +1,220 @@
+"""The op boundary on the GPU: what the read keeps, copies and traces.
+
+* Lifetimes (reference `tests/test_cuda.py:175-293`): after a completed
+  eager, compiled or graph-captured read (Full and Block source forms,
+  standard and sliced ranks, packed and list), no input tensor is kept alive
+  by the operator; only autograd holds arguments between forward and
+  backward.
+* Non-affine output batches (reference `tests/test_cuda.py:320-343`): a
+  transposed upstream gradient over a batch of tokens, eager and compiled.
+* No source stack on the list path (reference
+  `validation/source_checks.py:11-37`): a dispatch mode that fails on any
+  ``aten.stack`` / ``aten.cat`` whose inputs are the read's sources watches
+  an eager and a compiled list read, forward and backward.  A negative control
+  shows the guard catches the oracle's own stack.
+"""
+
+from __future__ import annotations
+
+import gc
+import weakref
+
+import pytest
+import torch
+from torch.utils._python_dispatch import TorchDispatchMode
+
+from attnres import attnres
+from helpers import SEEDS, both_oracles, compare_read, set_case
+from oracle.oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+# ---------------------------------------------------------------- lifetimes
+
+def _lifetime_refs(rank, mode, sequence):
+    values = [torch.randn(5, 17, device="cuda", dtype=torch.bfloat16, requires_grad=True) for _ in range(3)]
+    query = torch.randn(rank, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    refs = [weakref.ref(tensor) for tensor in (*values, query)]
+    inputs = tuple(values) if sequence else torch.stack(values)
+    if mode == "block":
+        partial = torch.randn_like(values[0], requires_grad=True)
+        refs.append(weakref.ref(partial))
+        inputs = (*inputs, partial) if sequence else torch.cat((inputs, partial[None]))
+    loss = attnres(inputs, query).square().sum()
+    # from here on only autograd may hold the arguments
+    del values, query, inputs
+    if mode == "block":
+        del partial
+    gc.collect()
+    loss.backward()
+    return refs
+
+
+@pytest.mark.parametrize("rank", [17, 5], ids=["standard", "sliced"])
+@pytest.mark.parametrize("mode", ["full", "block"])
+@pytest.mark.parametrize("sequence", [False, True])
+def test_eager_reads_release_their_inputs(rank, mode, sequence):
+    torch.manual_seed(SEEDS[0])
+    for _ in range(2):
+        refs = _lifetime_refs(rank, mode, sequence)
+        torch.cuda.synchronize()
+        gc.collect()
+        assert all(ref() is None for ref in refs), "a completed read kept an input tensor alive"
+
+
+def _compiled_lifetime_refs(compiled, rank, mode, graph):
+    values = tuple(torch.randn(5, 17, device="cuda", dtype=torch.bfloat16, requires_grad=True) for _ in range(3))
+    query = torch.randn(rank, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    partial = torch.randn_like(values[0], requires_grad=True) if mode == "block" else None
+    leaves = (*values, query, *((partial,) if partial is not None else ()))
+    refs = [weakref.ref(tensor) for tensor in leaves]
+
+    def step():
+        for tensor in leaves:
+            if tensor.grad is not None:
+                tensor.grad.zero_()
+        compiled(values, query, partial).backward()
+
+    if graph:
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):  # fresh leaves: their accumulators are made on this stream
+            step()
+            step()
+        stream.synchronize()
+        captured = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(captured, stream=stream):
+            step()
+        for _ in range(8):
+            with torch.no_grad():
+                for tensor in leaves:
+                    tensor.add_(0.01)
+            captured.replay()
+        torch.cuda.synchronize()
+        del captured, stream
+    else:
+        loss = compiled(values, query, partial)
+        del step, leaves, values, query, partial
+        gc.collect()
+        loss.backward()
+    return refs
+
+
+@pytest.mark.parametrize("rank", [17, 5], ids=["standard", "sliced"])
+@pytest.mark.parametrize("mode", ["full", "block"])
+@pytest.mark.parametrize("graph", [False, True], ids=["compiled", "compiled_graph"])
+def test_compiled_reads_release_their_inputs(rank, mode, graph):
+    counters = torch._dynamo.utils.counters
+
+    def forward(values, query, partial):
+        if mode == "full":
+            return attnres(values, query).square().sum()
+        return attnres((*values, partial), query).square().sum()
+
+    torch.manual_seed(SEEDS[0])
+    torch._dynamo.reset()
+    compiled = torch.compile(forward, fullgraph=True, dynamic=False)
+    graph_breaks = dict(counters["graph_break"])
+    graphs = None
+    for _ in range(2):
+        refs = _compiled_lifetime_refs(compiled, rank, mode, graph)
+        torch.cuda.synchronize()
+        gc.collect()
+        assert all(ref() is None for ref in refs), "a compiled read kept an input tensor alive"
+        assert dict(counters["graph_break"]) == graph_breaks
+        current = counters["stats"]["unique_graphs"]
+        assert graphs is None or current == graphs, "fresh inputs recompiled"
+        graphs = current
+
+
+# ------------------------------------------------------ non-affine batches
+
+@pytest.mark.parametrize("rank", [17, 5], ids=["standard", "sliced"])
+@pytest.mark.parametrize("sequence", [False, True])
+def test_non_affine_output_batches_keep_every_gradient(rank, sequence):
+    torch.manual_seed(SEEDS[0])
+    values = torch.randn(3, 2, 3, 17, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    query = torch.randn(rank, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    upstream = torch.randn(3, 2, 17, device="cuda", dtype=torch.bfloat16).transpose(0, 1)
+
+    def forward(v, q):
+        return attnres(tuple(v.unbind(0)) if sequence else v, q)
+
+    torch._dynamo.reset()
+    for label, function in (("eager", forward), ("compiled", torch.compile(forward, fullgraph=True, dynamic=False))):
+        set_case(f"non-affine batch R={rank} sequence={sequence} {label}")
+        actual = function(values, query)
+        grads = torch.autograd.grad(actual, (values, query), upstream)
+        expected, exact = both_oracles(lambda ls, q: (ls[0], q), [values], query, upstream)
+        compare_read((actual, *grads), expected, exact, ["out", "dv", "dq"], sources=3)
+
+
+# --------------------------------------------------------- no source stack
+
+class _SourceStackGuard(TorchDispatchMode):
+    """Fails on ``aten.stack`` / ``aten.cat`` of the read's sources: a list of
+    ``count`` (or ``count + 1``) tensors, all of one of the sources' shapes
+    (or that shape with a leading 1)."""
+
+    def __init__(self, shapes, count):
+        super().__init__()
+        self.shapes = {tuple(shape) for shape in shapes}
+        self.counts = {count, count + 1}
+        self.seen = 0
+
+    @classmethod
+    def ignore_compile_internals(cls):
+        return True  # watch the compiled artefact, not dynamo's own tracing
+
+    def _is_source(self, shape):
+        return shape in self.shapes or (len(shape) > 1 and shape[0] == 1 and shape[1:] in self.shapes)
+
+    def __torch_dispatch__(self, func, types, args=(), kwargs=None):
+        self.seen += 1
+        if func in (torch.ops.aten.stack.default, torch.ops.aten.cat.default) and args and args[0]:
+            shapes = [tuple(t.shape) for t in args[0]]
+            if len(shapes) in self.counts and len(set(shapes)) == 1 and self._is_source(shapes[0]):
+                raise AssertionError(f"the source-list path stacked its sources ({func})")
+        return func(*args, **(kwargs or {}))
+
+
+def _list_inputs(count, tokens, width, rank):
+    torch.manual_seed(SEEDS[2])
+    leaves = [torch.randn(tokens, width, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+              for _ in range(count)]
+    query = (torch.randn(rank, device="cuda", dtype=torch.bfloat16) * 0.25).requires_grad_()
+    upstream = torch.randn(tokens, width, device="cuda", dtype=torch.bfloat16)
+    return leaves, query, upstream
+
+
+@pytest.mark.parametrize("compiled", [False, True], ids=["eager", "compiled"])
+@pytest.mark.parametrize("count", [3, 9])
+def test_list_path_never_stacks_its_sources(count, compiled):
+    leaves, query, upstream = _list_inputs(count, 33, 256, 64)
+
+    def read(*args):
+        *sources, q = args
+        return attnres(tuple(sources), q)
+
+    torch._dynamo.reset()
+    function = torch.compile(read, fullgraph=True, dynamic=False) if compiled else read
+    if compiled:  # compile outside the guard, then run the artefact under it
+        function(*leaves, query)
+    guard = _SourceStackGuard([leaf.shape for leaf in leaves], count)
+    with guard:
+        out = function(*leaves, query)
+        grads = torch.autograd.grad(out, (*leaves, query), upstream)
+    assert guard.seen > 0, "the guard saw no dispatch"
+    set_case(f"no-stack guard count={count} compiled={compiled}")
+    expected, exact = both_oracles(lambda ls, q: (tuple(ls), q), leaves, query, upstream)
+    compare_read((out, *grads), expected, exact, ["out", *[f"dv{i}" for i in range(count)], "dq"], sources=count)
+
+
+def test_the_guard_catches_a_stacked_read():
+    """Negative control: the oracle stacks its list input, and the guard fails it."""
+    leaves = [torch.randn(7, 16, dtype=torch.bfloat16) for _ in range(3)]
+    query = torch.randn(16, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError, match="stacked its sources"):
+        with _SourceStackGuard([leaf.shape for leaf in leaves], 3):
+            oracle(tuple(leaves), query)

@@ -1,83 +1,155 @@
-"""The benchmark configurations at full size, checked through properties that
-do not depend on the size (the CPU oracle cannot run them whole in a test).
+"""The BASELINE configurations at full size against the CPU oracle.
 
-* Tokens are independent: a sample of token rows read on their own, through
-  the same kernels, gives bit-identical output rows and dv rows.
-* The sample against the CPU oracle, at the BF16 gate.
-* dq is a sum over tokens: the dq of the whole read equals the sum of the dq
-  of four token chunks, to BF16 rounding.
-* The output is a convex combination of the sources: every element lies
-  between the sources' minimum and maximum, up to the output's BF16 rounding.
+Every token row is compared.  The oracle runs over token chunks
+(`oracle.oracle_chunks`: the oracle's own graph per chunk; tokens are
+independent, so a chunk's output and value-gradient rows are exactly the
+whole read's), and the query gradient is the chunks' unrounded gradients
+summed and rounded once.  Bars (tests/helpers.py): the BF16 gate against the
+BF16 oracle, one BF16 ulp against the float64 oracle, and the saved
+statistics within 1e-5 relative of the oracle's.
 
-Shapes: c2 packed [25, 16384, 2048] R = 2048, c3 packed [16, 16384, 4096]
-R = 1024 (key masks), c4 a list of 9 separately allocated [32768, 2048].
+* c1: the CPU plumbing configuration's exact inputs (packed [8, 2, 512, 1024],
+  R = 1024, seed 0, drawn on the CPU by `bench.make_inputs` as
+  ``bench.py --config c1`` draws them).
+* c2 packed [25, 8x2048, 2048] R = 2048 and c3 packed [16, 16384, 4096]
+  R = 1024 with `bench.make_inputs` (per-source std U[0.5, 4], 1% of channels
+  x8); c4: 9 separately allocated [32768, 2048] sources (`bench.make_block_sources`),
+  its first read.  All rows against the float64 oracle too.
+* c5 subset at N = 16384: S in {1, 6, 7, 12, 13, 25, 48} x D in {1024, 4096}
+  x R in {D, D/4}, the first S sources of the tensor ``bench.py --config c5``
+  sweeps: every row and dq against the BF16 oracle (dq within one ulp of it:
+  both are FP32 sums rounded once), three 512-token samples against float64.
+
+Also at full size: a token sample read on its own gives bit-identical output
+and value-gradient rows (no interference between tokens at another grid size).
 """
 
 from __future__ import annotations
 
-import math
-
 import pytest
 import torch
 
+import bench
 from attnres import attnres
-from helpers import compare, oracle_grads
+from helpers import Streamed, check_statistics, compare, dv_floor, set_case
+from oracle.oracle import oracle_chunks
 
 pytestmark = pytest.mark.gpu
 
-CONFIGS = {"c2": (25, 16384, 2048, 2048, "packed"), "c3": (16, 16384, 4096, 1024, "packed"),
-           "c4": (9, 32768, 2048, 2048, "list")}
+_C5_SOURCES = (1, 6, 7, 12, 13, 25, 48)
 
 
-def _read(values, query, layout):
-    return attnres(tuple(values.unbind(0)) if layout == "list" else values, query)
+def _read(values, query, upstream, listed):
+    """The HIP read and its gradients; values packed [S, ..., D] or a list."""
+    if listed:
+        leaves = [v.detach().requires_grad_() for v in values]
+        q = query.detach().requires_grad_()
+        out = attnres(tuple(leaves), q)
+        grads = torch.autograd.grad(out, (*leaves, q), upstream)
+        return out, list(grads[:-1]), grads[-1]
+    leaf = values.detach().requires_grad_()
+    q = query.detach().requires_grad_()
+    out = attnres(leaf, q)
+    dv, dq = torch.autograd.grad(out, (leaf, q), upstream)
+    return out, dv, dq
 
 
-@pytest.mark.parametrize("name", sorted(CONFIGS))
-def test_full_size_read_properties(name):
-    sources, tokens, width, rank, layout = CONFIGS[name]
-    print(f"full size {name}: S={sources} N={tokens} D={width} R={rank} {layout}", flush=True)
+def _rows(values, listed, start, stop):
+    return [v[start:stop] for v in values] if listed else values[:, start:stop]
+
+
+def _stack(rows, listed):
+    return torch.stack(rows) if listed else rows
+
+
+def _check_full(values, query, upstream, *, listed, chunk=2048, exact_all=True):
+    """Every row of the read against the chunked oracle.  ``exact_all``: every
+    chunk and dq against float64 too; else three 512-token samples against
+    float64 and dq against the BF16 oracle."""
+    width = int(upstream.shape[-1])
+    tokens = int(values[0].shape[0]) if listed else values.numel() // (values.shape[0] * width)
+    flat = values if listed else values.reshape(values.shape[0], tokens, width)
+    g = upstream.reshape(tokens, width)
+    out, dv, dq = _read(flat, query, g, listed)
+    torch.cuda.synchronize()
+    sources = len(values) if listed else int(values.shape[0])
+    out_check, dv_check = Streamed("out"), Streamed("dv", dv_floor(sources))
+    dq32 = dq64 = None
+
+    def rows_of(start, stop, exact):
+        return next(oracle_chunks(_rows(flat, listed, start, stop), query, g[start:stop], chunk=stop - start,
+                                  exact=exact))
+
+    def add(start, stop, o, rows, o64=None, rows64=None):
+        out_check.add(out[start:stop], o, o64)
+        dv_check.add(_stack(_rows(dv, listed, start, stop), listed), _stack(rows, listed),
+                     None if rows64 is None else _stack(rows64, listed))
+
+    for start in range(0, tokens, chunk):
+        stop = min(tokens, start + chunk)
+        _, _, o, rows, q_part = rows_of(start, stop, False)
+        dq32 = q_part if dq32 is None else dq32 + q_part
+        o64 = rows64 = None
+        if exact_all:
+            _, _, o64, rows64, q64 = rows_of(start, stop, True)
+            dq64 = q64 if dq64 is None else dq64 + q64
+        add(start, stop, o, rows, o64, rows64)
+    if not exact_all:
+        for start in sorted({0, tokens // 2, max(0, tokens - 512)}):
+            stop = min(tokens, start + 512)
+            _, _, o, rows, _ = rows_of(start, stop, False)
+            _, _, o64, rows64, _ = rows_of(start, stop, True)
+            add(start, stop, o, rows, o64, rows64)
+    out_check.finish()
+    dv_check.finish()
+    metrics = compare(dq, dq32.to(torch.bfloat16), exact=dq64, name="dq")
+    if dq64 is None:
+        assert metrics["ulp_vs_oracle"] <= 1.0, f"dq: {metrics['ulp_vs_oracle']:.3f} ulps from the BF16 oracle"
+    check_statistics(flat, query)
+    return out, dv
+
+
+def _independent_sample(values, query, upstream, listed, out, dv):
+    """A token sample read on its own reproduces the full read's rows bit for bit."""
+    width = int(upstream.shape[-1])
+    tokens = int(values[0].shape[0]) if listed else values.numel() // (values.shape[0] * width)
+    flat = values if listed else values.reshape(values.shape[0], tokens, width)
     generator = torch.Generator(device="cuda").manual_seed(17)
-    scales = torch.rand(sources, 1, 1, generator=generator, device="cuda") * 3.5 + 0.5
-    values = torch.empty(sources, tokens, width, device="cuda", dtype=torch.bfloat16)
-    for s in range(sources):  # per source keeps the FP32 temporary small
-        values[s] = (torch.randn(tokens, width, generator=generator, device="cuda") * scales[s]).to(torch.bfloat16)
-    values.requires_grad_()
-    query = (torch.randn(rank, generator=generator, device="cuda") / math.sqrt(rank)).to(torch.bfloat16)
-    query.requires_grad_()
-    upstream = torch.randn(tokens, width, generator=generator, device="cuda").to(torch.bfloat16)
-
-    out = _read(values, query, layout)
-    grad_values, grad_query = torch.autograd.grad(out, (values, query), upstream)
-
-    # tokens are independent: a sample read on its own gives the same rows
     sample = torch.randperm(tokens, generator=generator, device="cuda")[:96].sort().values
-    sub_values = values.detach()[:, sample].contiguous().requires_grad_()
-    sub_out = _read(sub_values, query, layout)
-    sub_grad_values, _ = torch.autograd.grad(sub_out, (sub_values, query), upstream[sample])
-    assert torch.equal(sub_out, out[sample])
-    assert torch.equal(sub_grad_values, grad_values[:, sample])
+    part = [v[sample].contiguous() for v in flat] if listed else flat[:, sample].contiguous()
+    sub_out, sub_dv, _ = _read(part, query, upstream.reshape(tokens, width)[sample], listed)
+    assert torch.equal(sub_out, out.reshape(tokens, width)[sample])
+    full_dv = torch.stack(dv) if listed else dv.reshape(dv.shape[0], tokens, width)
+    assert torch.equal(_stack(sub_dv, listed), full_dv[:, sample])
 
-    # the sample against the oracle
-    def make(leaves, q):
-        return (tuple(leaves[0].unbind(0)) if layout == "list" else leaves[0]), q
 
-    expected, (expected_values, _) = oracle_grads(make, [sub_values], query, upstream[sample])
-    compare(sub_out, expected)
-    compare(sub_grad_values, expected_values)
+@pytest.mark.parametrize("name", ["c1", "c2", "c3"])
+def test_packed_config_every_row_matches_oracle(name):
+    cfg = bench.CONFIGS[name]
+    print(f"full size {name}: {cfg['name']}", flush=True)
+    set_case(f"{name} full size")
+    values, query, upstream = bench.make_inputs(cfg, "cuda", seed=0)
+    out, dv = _check_full(values, query, upstream, listed=False)
+    _independent_sample(values, query, upstream, False, out, dv)
 
-    # dq is a sum over tokens: four chunks add up to the whole read's dq
-    chunk_sum = torch.zeros(rank, device="cuda")
-    for chunk in torch.arange(tokens, device="cuda").chunk(4):
-        part = values.detach()[:, chunk].contiguous()
-        part_out = _read(part, query, layout)
-        chunk_sum += torch.autograd.grad(part_out, query, upstream[chunk])[0].float()
-    torch.testing.assert_close(chunk_sum, grad_query.float(), rtol=2.0**-6,
-                               atol=2.0**-6 * float(grad_query.float().abs().max()))
 
-    # convexity, up to the output's rounding (half a BF16 ulp of the bound)
-    low = values.detach().amin(0).float()
-    high = values.detach().amax(0).float()
-    slack = torch.maximum(low.abs(), high.abs()) * 2.0**-8
-    result = out.float()
-    assert bool(((result >= low - slack) & (result <= high + slack)).all())
+def test_block_list_config_every_row_matches_oracle():
+    cfg = bench.CONFIGS["c4"]
+    print(f"full size c4: {cfg['name']}", flush=True)
+    set_case("c4 full size (first read)")
+    sources, queries, upstreams = bench.make_block_sources(cfg, "cuda", seed=0)
+    out, dv = _check_full(sources, queries[0], upstreams[0], listed=True)
+    _independent_sample(sources, queries[0], upstreams[0], True, out, dv)
+
+
+@pytest.mark.parametrize("width,rank", [(1024, 1024), (1024, 256), (4096, 4096), (4096, 1024)],
+                         ids=lambda v: str(v))
+def test_sweep_subset_matches_oracle(width, rank):
+    tokens = bench.CONFIGS["c5"]["batch"][0]
+    values, query, upstream = bench.make_inputs(dict(sources=max(_C5_SOURCES), batch=(tokens,), width=width,
+                                                     rank=rank), "cuda", seed=width + rank)
+    for sources in _C5_SOURCES:
+        print(f"c5 subset S={sources} N={tokens} D={width} R={rank}", flush=True)
+        set_case(f"c5 S={sources} D={width} R={rank}")
+        _check_full(values[:sources], query, upstream, listed=False, chunk=2048 if width <= 1024 else 1024,
+                    exact_all=False)

@@ -8,7 +8,10 @@ per-source strides and a duplicated source (`tests/test_api.py:112-142`),
 exact known-answer cases (`validation/softmax_checks.py:9-30`,
 `tests/test_routing_checks.py`), bitwise replay
 (`tests/test_bf16_packed_kernels.py:90-94`) and >2^31 offsets
-(`tests/test_offsets.py`).  Bar: the reference's BF16 gate rtol=atol=0.05.
+(`tests/test_offsets.py`).  Bars: the reference's BF16 gate rtol=atol=0.05
+against the BF16 oracle, one BF16 ulp against the float64 oracle (out, dv,
+dq), and the saved statistics (logit, 1/rms, max, 1/sum) within 1e-5
+relative of the oracle's (tests/helpers.py).
 """
 
 from __future__ import annotations
@@ -19,7 +22,7 @@ import pytest
 import torch
 
 from attnres import attnres
-from helpers import SEEDS, compare, oracle_grads
+from helpers import SEEDS, both_oracles, check_statistics, compare, compare_read, oracle_grads, set_case
 
 pytestmark = pytest.mark.gpu
 
@@ -49,11 +52,14 @@ def _strided_case(shape, layout, seed):
 
     values, q = make([producer], query)
     print(f"case shape={shape} layout={layout} seed={seed}", flush=True)
+    set_case(f"strided {shape} {layout}")
     actual = attnres(values, q)
     grads = torch.autograd.grad(actual, (producer, query), upstream)
-    expected, expected_grads = oracle_grads(make, [producer], query, upstream)
+    expected, exact = both_oracles(make, [producer], query, upstream)
     torch.cuda.synchronize()
-    return [compare(a, e) for a, e in zip((actual, *grads), (expected, *expected_grads))]
+    metrics = compare_read((actual, *grads), expected, exact, ["out", "dv", "dq"], sources=s)
+    check_statistics(values, q.detach())
+    return metrics
 
 
 @pytest.mark.parametrize("layout", ["packed", "list"])
@@ -82,11 +88,12 @@ def test_aligned_fast_path_matches_oracle(width, rank, layout):
     def make(leaves, q):
         return (tuple(leaves[0].unbind(0)) if layout == "list" else leaves[0]), q
 
+    set_case(f"aligned D={width} R={rank} {layout}")
     actual = attnres(make([values], query)[0], query)
     grads = torch.autograd.grad(actual, (values, query), upstream)
-    expected, expected_grads = oracle_grads(make, [values], query, upstream)
-    for a, e in zip((actual, *grads), (expected, *expected_grads)):
-        compare(a, e)
+    expected, exact = both_oracles(make, [values], query, upstream)
+    compare_read((actual, *grads), expected, exact, ["out", "dv", "dq"], sources=s)
+    check_statistics(make([values.detach()], query)[0], query.detach())
 
 
 @pytest.mark.parametrize("layout", ["packed", "list"])
@@ -110,11 +117,11 @@ def test_backward_ring_depths_match_oracle(tokens, width, rank, layout):
         return (tuple(leaves[0].unbind(0)) if layout == "list" else leaves[0]), q
 
     print(f"ring depths N={tokens} D={width} R={rank} layout={layout}", flush=True)
+    set_case(f"ring N={tokens} D={width} R={rank} {layout}")
     actual = attnres(make([values], query)[0], query)
     grads = torch.autograd.grad(actual, (values, query), upstream)
-    expected, expected_grads = oracle_grads(make, [values], query, upstream)
-    for a, e in zip((actual, *grads), (expected, *expected_grads)):
-        compare(a, e)
+    expected, exact = both_oracles(make, [values], query, upstream)
+    compare_read((actual, *grads), expected, exact, ["out", "dv", "dq"], sources=s)
 
 
 @pytest.mark.parametrize("container", ["list", "tuple", "packed_values"])
@@ -140,11 +147,14 @@ def test_source_containers_with_per_source_strides(container):
             values = torch.stack(values)
         return values, q[::2]
 
+    set_case(f"containers {container}")
     actual = attnres(*make(leaves, query))
     grads = torch.autograd.grad(actual, (*leaves, query), upstream)
-    expected, expected_grads = oracle_grads(make, leaves, query, upstream)
-    for a, e in zip((actual, *grads), (expected, *expected_grads)):
-        compare(a, e)
+    expected, exact = both_oracles(make, leaves, query, upstream)
+    # the duplicated source's gradient is autograd's BF16 sum of two reads' rows
+    compare_read((actual, *grads[1:]), (expected[0], *expected[2:]), (exact[0], *exact[2:]),
+                 ["out", "dv1", "dv2", "dq"], sources=4)
+    compare(grads[0], expected[1], name="dv0+dv3")
 
 
 @pytest.mark.parametrize("packed", [False, True])
@@ -276,11 +286,11 @@ def test_source_offsets_above_int32():
     values.requires_grad_()
     query = (torch.randn(rank, device="cuda", dtype=torch.bfloat16) * 0.25).requires_grad_()
     upstream = torch.randn(1, width, device="cuda", dtype=torch.bfloat16)
+    set_case("source offsets > 2^31")
     actual = attnres(values, query)
     grads = torch.autograd.grad(actual, (values, query), upstream)
-    expected, expected_grads = oracle_grads(lambda ls, q: (ls[0], q), [values], query, upstream)
-    for a, e in zip((actual, *grads), (expected, *expected_grads)):
-        compare(a, e)
+    expected, exact = both_oracles(lambda ls, q: (ls[0], q), [values], query, upstream)
+    compare_read((actual, *grads), expected, exact, ["out", "dv", "dq"], sources=2)
     del storage
 
 
@@ -298,10 +308,9 @@ def test_source_list_row_stride_above_int32(rank):
     other = torch.randn(2, width, device="cuda", dtype=torch.bfloat16, requires_grad=True)
     query = (torch.randn(rank, device="cuda", dtype=torch.bfloat16) * 0.25).requires_grad_()
     upstream = torch.randn(2, width, device="cuda", dtype=torch.bfloat16)
+    set_case(f"list row stride > 2^31 R={rank}")
     actual = attnres((value, other), query)
     grads = torch.autograd.grad(actual, (value, other, query), upstream)
-    expected, expected_grads = oracle_grads(
-        lambda ls, q: (tuple(ls), q), [value, other], query, upstream)
-    for a, e in zip((actual, *grads), (expected, *expected_grads)):
-        compare(a, e)
+    expected, exact = both_oracles(lambda ls, q: (tuple(ls), q), [value, other], query, upstream)
+    compare_read((actual, *grads), expected, exact, ["out", "dv0", "dv1", "dq"], sources=2)
     del storage

@@ -20,7 +20,7 @@ import pytest
 import torch
 
 from attnres import _ops, attnres
-from helpers import SEEDS, compare, oracle_grads
+from helpers import SEEDS, both_oracles, check_statistics, compare_read, set_case
 
 pytestmark = pytest.mark.gpu
 
@@ -54,12 +54,13 @@ def test_recompute_backward_matches_oracle(sources, width, rank, padded, layout)
         return (tuple(values.unbind(0)) if layout == "list" else values), q
 
     print(f"recompute S={sources} D={width} R={rank} padded={padded} layout={layout}", flush=True)
+    set_case(f"recompute S={sources} D={width} R={rank} padded={padded} {layout}")
     actual = attnres(make([producer], query)[0], query)
     grads = torch.autograd.grad(actual, (producer, query), upstream)
-    expected, expected_grads = oracle_grads(make, [producer], query, upstream)
+    expected, exact = both_oracles(make, [producer], query, upstream)
     torch.cuda.synchronize()
-    for a, e in zip((actual, *grads), (expected, *expected_grads)):
-        compare(a, e)
+    compare_read((actual, *grads), expected, exact, ["out", "dv", "dq"], sources=sources)
+    check_statistics(make([producer.detach()], query)[0], query.detach())
 
 
 @pytest.mark.parametrize("layout", ["packed", "list"])

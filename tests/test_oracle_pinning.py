@@ -30,7 +30,8 @@ import pytest
 import torch
 
 from oracle import exact
-from oracle.oracle import EPS, oracle, oracle_with_grads, softmax_statistics
+from oracle.oracle import (EPS, chunked_with_grads, exact_with_grads, oracle, oracle_float64, oracle_with_grads,
+                           softmax_statistics)
 
 BF16_ULP = 2.0**-8  # relative spacing of BF16 (8 significant bits)
 
@@ -234,3 +235,60 @@ def test_autocast_does_not_change_the_oracle(sequence):
 def test_oracle_rejects_other_floating_dtypes(dtype):
     with pytest.raises(TypeError, match="requires BF16"):
         oracle(torch.ones(2, 3, 16, dtype=dtype), torch.ones(16, dtype=dtype))
+
+
+# ----------------------------------------------------- float64 and chunked
+
+@pytest.mark.parametrize("seed,shape,scale,eps", [
+    (20260827, (3, 4, 12, 12), 1.0, EPS),
+    (20260911, (2, 6, 9, 3), -1.5, 2.0**-10),
+    (7, (7, 2, 24, 24), 4.0, 1e-3),
+])
+def test_float64_oracle_matches_brute_force_and_finite_differences(seed, shape, scale, eps):
+    sources, tokens, width, rank = shape
+    values, query, upstream = _case(seed, sources, tokens, width, rank)
+    out, grad_values, grad_query = exact_with_grads(values, query, upstream, eps=eps, scale=scale)
+    assert out.dtype == grad_values.dtype == grad_query.dtype == torch.float64
+    expected = exact.read(_f64(values), _f64(query), eps, scale)
+    np.testing.assert_allclose(out.numpy(), expected, rtol=1e-12, atol=1e-13)
+    fd_values, fd_query = exact.gradients(_f64(values), _f64(query), _f64(upstream), eps, scale)
+    scale_v, scale_q = np.abs(fd_values).max(), np.abs(fd_query).max()
+    np.testing.assert_allclose(grad_values.numpy(), fd_values, rtol=1e-6, atol=1e-7 * scale_v)
+    np.testing.assert_allclose(grad_query.numpy(), fd_query, rtol=1e-6, atol=1e-7 * scale_q)
+    # the BF16 oracle is the float64 one plus its roundings
+    _within_bf16(oracle(values, query, eps=eps, scale=scale), out.numpy(), ulps=1.0, floor=1e-6)
+
+
+def test_float64_oracle_rejects_planted_mistakes():
+    """A wrong-axis softmax or a first-R key in float64 fails the 1e-12 check."""
+    values, query, _ = _case(99, 4, 3, 12, 6)
+    expected = exact.read(_f64(values), _f64(query), EPS, 1.0)
+    good = oracle_float64(values.double(), query.double())
+    np.testing.assert_allclose(good.numpy(), expected, rtol=1e-12, atol=1e-13)
+    for kind in ("first_r_key", "wrong_axis", "sign"):
+        bad = _mutant(kind)(values, query).double().numpy()  # BF16 mutant: far beyond 1e-12
+        with pytest.raises(AssertionError):
+            np.testing.assert_allclose(bad, expected, rtol=1e-4, atol=1e-4)
+
+
+def test_float64_oracle_rejects_other_dtypes():
+    with pytest.raises(TypeError, match="float64"):
+        oracle_float64(torch.ones(2, 3, 16, dtype=torch.bfloat16), torch.ones(16, dtype=torch.bfloat16))
+
+
+@pytest.mark.parametrize("listed", [False, True])
+def test_chunked_oracle_equals_the_whole_read(listed):
+    values, query, upstream = _case(23, 5, 37, 24, 10)
+    whole = oracle_with_grads(list(values.unbind()) if listed else values, query, upstream, scale=0.8)
+    chunked = chunked_with_grads(list(values.unbind()) if listed else values, query, upstream, scale=0.8,
+                                 chunk=8)
+    assert torch.equal(chunked[0], whole[0])
+    grads = torch.stack(chunked[1]) if listed else chunked[1]
+    expected = torch.stack(whole[1]) if listed else whole[1]
+    assert torch.equal(grads, expected)
+    # dq: FP32 chunk sums rounded once, against one FP32 sum rounded once
+    torch.testing.assert_close(chunked[2].float(), whole[2].float(), rtol=BF16_ULP, atol=0)
+    exact_whole = exact_with_grads(values, query, upstream, scale=0.8)
+    exact_chunked = chunked_with_grads(values, query, upstream, scale=0.8, chunk=8, exact=True)
+    for a, e in zip(exact_chunked, exact_whole):
+        np.testing.assert_allclose(a.numpy(), e.numpy(), rtol=1e-12, atol=1e-13)
