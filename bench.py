@@ -602,8 +602,10 @@ def run_model(cfg: dict, steps: int, warmup: int, variant: str = "both", autocas
     source-bank step with gathered gradients, with accumulated gradients and
     with inductor-compiled sublayers; "plain", "bank", "bank_accumulate" or
     "bank_compiled" times one of them alone (for traces), "compiled" the plain
-    model under whole-model inductor compilation. A config with "autocast"
-    always runs under BF16 autocast.
+    model under whole-model inductor compilation, "graph" the whole step
+    (compiled model and loss under BF16 autocast, fused capturable AdamW)
+    captured in one HIP graph and replayed (benchmarks/training_graph.py). A
+    config with "autocast" always runs under BF16 autocast.
     """
     autocast = autocast or cfg.get("autocast", False)
     import torch
@@ -645,6 +647,26 @@ def run_model(cfg: dict, steps: int, warmup: int, variant: str = "both", autocas
         torch.cuda.synchronize()
         return start.elapsed_time(stop) / steps, float(loss)
 
+    def time_graph():
+        from benchmarks.training_graph import capture_training_step
+
+        torch.manual_seed(0)
+        model = make_model(config, backend="kernel").cuda()
+        optimizer = torch.optim.AdamW(model.parameters(), lr=1e-4, fused=True, capturable=True)
+        torch._dynamo.reset()
+        captured = capture_training_step(model, optimizer, tokens, targets)
+        for _ in range(warmup):
+            captured.replay()
+        torch.cuda.synchronize()
+        start, stop = _event(), _event()
+        start.record()
+        for _ in range(steps):
+            loss = captured.replay()
+        stop.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) / steps, float(loss)
+
+    graph_ms, graph_loss = time_graph() if variant == "graph" else (None, None)
     ms, loss = time_steps(False) if variant in ("both", "plain") else (None, None)
     bank_ms, bank_loss = time_steps(True) if variant in ("both", "bank") else (None, None)
     acc_ms, acc_loss = time_steps(True, "accumulate") if variant in ("both", "bank_accumulate") else (None, None)
@@ -658,6 +680,9 @@ def run_model(cfg: dict, steps: int, warmup: int, variant: str = "both", autocas
     def rounded(x, digits):
         return None if x is None else round(x, digits)
 
+    timed_name, timed_ms = next(((name, t) for name, t in (("plain", ms), ("graph", graph_ms), ("compiled", comp_ms),
+                                                            ("bank", bank_ms), ("bank_accumulate", acc_ms),
+                                                            ("bank_compiled", bc_ms)) if t is not None), (None, None))
     counts = read_sources_per_step(config)
     reads = len(counts)
     read_bytes_per_step = sum(sum(read_bytes(s, n_tokens, config.width)) for s in counts)
@@ -665,9 +690,10 @@ def run_model(cfg: dict, steps: int, warmup: int, variant: str = "both", autocas
     return {
         "metric": f"model: {config.layers}-layer {schedule} causal LM training step ({reads} AttnRes reads, "
                   f"S={min(counts)}..{max(counts)}), tokens/s",
-        "value": rate(ms), "unit": "tokens/s", "n_gpus": 1, "steps": steps,
-        "warmup": warmup, "ms_per_step": rounded(ms, 3), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16 autocast" if autocast else "f32 model, bf16 reads",
+        # the plain step's rate, or the one variant timed on its own
+        "value": rate(timed_ms), "value_variant": timed_name, "unit": "tokens/s", "n_gpus": 1, "steps": steps,
+        "warmup": warmup, "ms_per_step": rounded(timed_ms, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16 autocast" if autocast or graph_ms is not None else "f32 model, bf16 reads",
         "data": "synthetic tokens (seeded)",
         "config": {"workload": cfg["name"], "layers": config.layers, "width": config.width, "heads": config.heads,
                    "ffn": config.ffn, "batch": config.batch, "sequence": config.sequence, "vocab": config.vocab,
@@ -689,6 +715,8 @@ def run_model(cfg: dict, steps: int, warmup: int, variant: str = "both", autocas
                                         "loss": rounded(bc_loss, 4)},
         # --model-variant compiled: the plain model under torch.compile(fullgraph=True) (inductor)
         "compiled": {"ms_per_step": rounded(comp_ms, 3), "tokens_per_s": rate(comp_ms), "loss": rounded(comp_loss, 4)},
+        # --model-variant graph: the whole step captured in one HIP graph (BF16 autocast)
+        "graph": {"ms_per_step": rounded(graph_ms, 3), "tokens_per_s": rate(graph_ms), "loss": rounded(graph_loss, 4)},
         "roofline": None,
         "cpu_baseline": None,
     }
@@ -707,7 +735,7 @@ def main(argv=None) -> int:
                         help="--config model / model_block: run the steps under torch.autocast (BF16), as the "
                              "reference's 24-layer timings do")
     parser.add_argument("--model-variant",
-                        choices=("both", "plain", "bank", "bank_accumulate", "bank_compiled", "compiled"),
+                        choices=("both", "plain", "bank", "bank_accumulate", "bank_compiled", "compiled", "graph"),
                         default="both",
                         help="--config model / model_block: time the plain step, the source-bank step (gathered "
                              "or accumulated gradients, or with compiled sublayers), all four (both), or the plain "

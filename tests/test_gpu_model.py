@@ -192,3 +192,100 @@ def test_bf16_autocast_model_with_and_without_the_bank(mode):
         with torch.autocast("cuda", dtype=torch.bfloat16):
             losses.append(float(training_step(banked, optimizer, tokens, targets)))
     assert losses[-1] < losses[0]
+
+
+@pytest.mark.parametrize("layout", ["packed", "list"])
+@pytest.mark.parametrize("mode", ["full", "block"])
+def test_checkpointed_compiled_model_matches_oracle_model(mode, layout):
+    """Activation checkpointing through the reads (reference
+    validation/training_checks.py:35-37, 79-88): the model under
+    torch.utils.checkpoint(..., use_reentrant=False) inside
+    torch.compile(fullgraph=True) against the oracle-backed model on the same
+    weights, and against the same HIP model without checkpointing.  With 3
+    layers the Full schedule reads 1..7 sources, so both the recompute reads
+    (S <= 6) and a saving read (S = 7) run their forward twice (once more in
+    the backward's recomputation)."""
+    from torch.utils.checkpoint import checkpoint
+
+    config = _config(mode, layout, "standard")
+    print(f"checkpointed compiled model mode={mode} layout={layout}", flush=True)
+    torch.manual_seed(31)
+    reference = make_model(config, backend=oracle)
+    candidate = make_model(config, backend="kernel")
+    candidate.load_state_dict(reference.state_dict())
+    candidate.cuda()
+    plain = copy.deepcopy(candidate)
+    tokens = torch.randint(config.vocab, (config.batch, config.sequence))
+    weight = torch.randn(config.batch, config.sequence, config.vocab)
+    torch._dynamo.reset()
+    checked = torch.compile(lambda x: checkpoint(candidate, x, use_reentrant=False), fullgraph=True, dynamic=False)
+    actual = checked(tokens.cuda())
+    expected = reference(tokens)
+    baseline = plain(tokens.cuda())
+    assert _relative_error(actual.cpu(), expected) < 2e-2
+    # inductor reorders the FP32 work around the reads, which can move a read's BF16 rounding
+    assert _relative_error(actual, baseline) < 1e-2
+    (expected * weight).sum().backward()
+    (actual * weight.cuda()).sum().backward()
+    (baseline * weight.cuda()).sum().backward()
+    for (name, p), q, b in zip(candidate.named_parameters(), reference.parameters(), plain.parameters()):
+        assert p.grad is not None, name
+        assert _relative_error(p.grad.cpu(), q.grad) < 5e-2, name
+        assert _relative_error(p.grad, b.grad) < 2e-2, name
+
+
+@pytest.mark.parametrize("gradients", ["gather", "accumulate"])
+@pytest.mark.parametrize("mode", ["full", "block"])
+def test_checkpointed_bank_model_matches_the_bank_model(mode, gradients):
+    """The source-bank model (eager) under torch.utils.checkpoint(...,
+    use_reentrant=False): the backward re-runs the forward, building a second
+    bank whose reads give the same bits; gradients equal the bank model's
+    without checkpointing."""
+    from torch.utils.checkpoint import checkpoint
+
+    config = _config(mode, "packed", "standard")
+    print(f"checkpointed bank model mode={mode} gradients={gradients}", flush=True)
+    torch.manual_seed(37)
+    model = make_model(config, backend="kernel", source_bank=True, bank_gradients=gradients).cuda()
+    other = copy.deepcopy(model)
+    tokens = torch.randint(config.vocab, (config.batch, config.sequence), device="cuda")
+    weight = torch.randn(config.batch, config.sequence, config.vocab, device="cuda")
+    a = checkpoint(model, tokens, use_reentrant=False)
+    b = other(tokens)
+    assert torch.equal(a, b)
+    (a * weight).sum().backward()
+    (b * weight).sum().backward()
+    for (name, p), q in zip(model.named_parameters(), other.parameters()):
+        assert p.grad is not None, name
+        torch.testing.assert_close(p.grad, q.grad, rtol=1e-5, atol=1e-7, msg=name)
+
+
+@pytest.mark.parametrize("mode", ["full", "block"])
+def test_captured_training_step_matches_compiled_steps(mode):
+    """A whole training step in one HIP graph (benchmarks/training_graph.py:
+    compiled model and loss under BF16 autocast, two accumulated microbatches,
+    fused capturable AdamW): three replays on changed batches give the losses
+    and parameters of three compiled steps run eagerly from the same start."""
+    from benchmarks.training_graph import _loss, _step, capture_training_step
+
+    config = _config(mode, "packed", "standard")
+    print(f"captured training step mode={mode}", flush=True)
+    torch.manual_seed(41)
+    model = make_model(config, backend="kernel").cuda()
+    twin = copy.deepcopy(model)
+    optimizer = torch.optim.AdamW(model.parameters(), lr=1e-3, fused=True, capturable=True)
+    twin_optimizer = torch.optim.AdamW(twin.parameters(), lr=1e-3, fused=True, capturable=True)
+    batches = [(torch.randint(config.vocab, (2 * config.batch, config.sequence), device="cuda"),
+                torch.randint(config.vocab, (2 * config.batch, config.sequence), device="cuda")) for _ in range(3)]
+    torch._dynamo.reset()
+    captured = capture_training_step(model, optimizer, *batches[0], accumulation=2)
+    twin_model = torch.compile(twin, fullgraph=True, dynamic=False)
+    twin_loss = torch.compile(_loss, fullgraph=True, dynamic=False)
+    for index, (tokens, targets) in enumerate(batches):
+        captured.copy_inputs(tokens, targets)
+        loss = captured.replay().clone()
+        expected = _step(twin_model, twin_loss, twin_optimizer, tokens, targets, 2)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(loss, expected.detach(), rtol=1e-4, atol=1e-5, msg=f"step {index}")
+    for (name, p), q in zip(model.named_parameters(), twin.parameters()):
+        torch.testing.assert_close(p, q, rtol=1e-4, atol=1e-6, msg=name)
