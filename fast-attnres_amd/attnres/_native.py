@@ -41,6 +41,10 @@ SIGNATURES = {
         _c_void_p, _i64, _i64, _i64, _i64, _i64, _c_void_p, _i64, _f32,
         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
         _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p]),
+    "attnres_hip_packed_backward_noalloc": (ctypes.c_int, [
+        _c_void_p, _i64, _i64, _i64, _i64, _i64, _c_void_p, _i64, _f32,
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+        _c_void_p, _c_void_p, _c_void_p]),
     "attnres_hip_sources_forward": (ctypes.c_int, [
         _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _f32, _f32,
         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p]),

@@ -18,9 +18,19 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <mutex>
 #include <type_traits>
 
 #include "attnres_internal.h"
+
+// The dq workspace of attnres_hip_packed_backward_noalloc: device memory the
+// library holds for the life of the process, one copy per GPU (4 MiB each).
+// Its host-side name is not a device address: host code uses the address
+// hipGetSymbolAddress returns on each device (attnres_hip::device_scratch).
+// Nothing in it needs clearing: every backward workgroup writes its whole
+// dq partial row, and the reduction reads only the rows of its own launch.
+static constexpr int64_t kScratchElems = int64_t{1} << 20;  // FP32
+static __device__ __align__(256) float scratch[kScratchElems];
 
 namespace attnres_hip {
 
@@ -379,13 +389,17 @@ int attnres_hip_packed_forward(const void* values, int64_t source_stride, int64_
 namespace attnres_hip {
 namespace {
 
+// `fit_grid`: a workspace smaller than workspace_elems() caps the backward's
+// grid at the partial rows it holds (at least one) instead of being rejected
+// -- the kernels stride over tokens, so any grid gives the same dv, and dq
+// differs only in the FP32 order of the per-workgroup sums.
 template <class Grads = PackedGrads>
 int packed_backward(const void* values, int64_t source_stride, int64_t row_stride, int64_t n_sources,
                     int64_t n_tokens, int64_t width, const void* query, int64_t rank, float scale,
                     const void* out, const int8_t* out_refine, const void* grad_out, const float* logit,
                     const float* inv_rms, const float* stats, void* grad_values, void* grad_query,
                     float* dq_workspace, int64_t dq_workspace_elems, const uint8_t* accumulate, bool need_flags,
-                    void* stream) {
+                    void* stream, bool fit_grid = false) {
   constexpr bool kF32 = kF32Grads<Grads>;
   constexpr bool kCoef = std::is_same_v<Grads, CoefSink>;
   const char* name = kCoef ? "attnres_hip_packed_backward_coef"
@@ -401,9 +415,10 @@ int packed_backward(const void* values, int64_t source_stride, int64_t row_strid
   if (source_stride < 0 || row_stride < 0) return fail(ATTNRES_ERR_STRIDE, "negative stride");
   if ((st = check_scalars(1.0f, scale, false))) return st;
   const int64_t need = workspace_elems(n_tokens, width, rank);
-  if (dq_workspace_elems < need)
+  if (dq_workspace_elems < (fit_grid ? 2 * rank : need))
     return fail(ATTNRES_ERR_WORKSPACE, "dq workspace has %lld elements, needs %lld",
-                (long long)dq_workspace_elems, (long long)need);
+                (long long)dq_workspace_elems, (long long)(fit_grid ? 2 * rank : need));
+  const int64_t rows = std::min(need, dq_workspace_elems) / rank - 1;  // partial rows; the total follows
   BwdArgs<PackedRows, Grads> a{};
   a.src = PackedRows{static_cast<const uint16_t*>(values), source_stride, row_stride};
   if constexpr (kCoef) {
@@ -421,7 +436,7 @@ int packed_backward(const void* values, int64_t source_stride, int64_t row_strid
   a.inv_rms = inv_rms;
   a.stats = stats;
   a.partial = dq_workspace;
-  a.max_grid = need / rank - 1;
+  a.max_grid = rows;
   a.n_tokens = n_tokens;
   a.n_sources = static_cast<int>(n_sources);
   a.width = static_cast<int>(width);
@@ -431,15 +446,69 @@ int packed_backward(const void* values, int64_t source_stride, int64_t row_strid
                    aligned16_or_null(out_refine) && aligned16(grad_out) && (kCoef || aligned16(grad_values)) &&
                    (source_stride % kVec == 0 || n_sources == 1) && (row_stride % kVec == 0 || n_tokens == 1);
   const bool acc = set_accumulate(a, accumulate, n_sources);
-  float* dq32 = dq_workspace + (need - rank);  // after the partial rows
+  float* dq32 = dq_workspace + rows * rank;  // after the partial rows
   return launch_backward(a, vec, acc, recompute, dq32, static_cast<uint16_t*>(grad_query),
                          static_cast<hipStream_t>(stream));
+}
+
+// ------------------------------------------------- scratch of the no-alloc entry
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+float* g_scratch[kMaxDevices] = {};
+
+// The current device's copy of `scratch`, looked up on its first use there
+// (with that device current, as the caller's stream requires).
+int device_scratch(float** ptr) {
+  int device = 0;
+  hipError_t e = hipGetDevice(&device);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(ATTNRES_ERR_LAUNCH, "hipGetDevice failed: %s", hipGetErrorString(e));
+  }
+  if (device < 0 || device >= kMaxDevices)
+    return fail(ATTNRES_ERR_LAUNCH, "device %d outside 0..%d", device, kMaxDevices - 1);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch[device]) {
+    void* address = nullptr;
+    e = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !address) {
+      (void)hipGetLastError();
+      return fail(ATTNRES_ERR_LAUNCH, "hipGetSymbolAddress(scratch) on device %d failed: %s", device,
+                  hipGetErrorString(e));
+    }
+    g_scratch[device] = static_cast<float*>(address);
+  }
+  *ptr = g_scratch[device];
+  return ATTNRES_OK;
 }
 
 }  // namespace
 }  // namespace attnres_hip
 
 extern "C" {
+
+int attnres_hip_packed_backward_noalloc(const void* values, int64_t source_stride, int64_t row_stride,
+                                        int64_t n_sources, int64_t n_tokens, int64_t width,
+                                        const void* query, int64_t rank, float scale, const void* out,
+                                        const int8_t* out_refine, const void* grad_out,
+                                        const float* logit, const float* inv_rms, const float* stats,
+                                        void* grad_values, void* grad_query, void* stream) {
+  int st = check_shape(n_sources, n_tokens, width, rank);
+  if (st) return st;
+  if (2 * rank > kScratchElems)
+    return fail(ATTNRES_ERR_WORKSPACE, "rank=%lld needs more than the %lld-element scratch", (long long)rank,
+                (long long)kScratchElems);
+  // the pointer checks of the workspace entry point, before any runtime call
+  if (!values || !query || (out_refine && !out) || !grad_out || !logit || !inv_rms || !stats || !grad_values ||
+      !grad_query)
+    return fail(ATTNRES_ERR_NULL_POINTER, "null pointer argument to attnres_hip_packed_backward_noalloc");
+  float* workspace = nullptr;
+  if ((st = device_scratch(&workspace))) return st;
+  return packed_backward(values, source_stride, row_stride, n_sources, n_tokens, width, query, rank, scale, out,
+                         out_refine, grad_out, logit, inv_rms, stats, grad_values, grad_query, workspace,
+                         kScratchElems, nullptr, false, stream, true);
+}
 
 int attnres_hip_packed_backward(const void* values, int64_t source_stride, int64_t row_stride,
                                 int64_t n_sources, int64_t n_tokens, int64_t width,

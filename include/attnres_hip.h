@@ -143,6 +143,34 @@ int attnres_hip_packed_backward(const void* values, int64_t source_stride,
                                 int64_t dq_workspace_elems, void* stream);
 
 /*
+ * Packed backward that allocates nothing and takes no workspace: the same
+ * arguments, kernels and results as attnres_hip_packed_backward without
+ * dq_workspace / dq_workspace_elems.  The dq partial rows live in a 4 MiB
+ * device array that the library holds for the life of the process, one per
+ * GPU (looked up on the first call on each device, which must be current).
+ * When the grid would need more partial rows than that array holds
+ * ((rows + 1) * rank > 2^20 FP32 elements), the backward runs on fewer
+ * workgroups: dv is the same bits, dq may differ in the FP32 order of its
+ * partial sums.  rank must be at most 2^19 (always so within the envelope),
+ * else ATTNRES_ERR_WORKSPACE.  Calls on one GPU share that array, so calls
+ * that overlap in time on one GPU (concurrent streams, threads) race; calls
+ * in stream order do not.
+ *
+ * No counterpart in the reference (its backward allocates dq partials with
+ * torch.empty, fixed_tail.py:980-984).  For callers that cannot allocate
+ * device memory: code under stream capture, tight serving loops, harnesses
+ * that forbid hipMalloc.
+ */
+int attnres_hip_packed_backward_noalloc(const void* values, int64_t source_stride,
+                                        int64_t row_stride, int64_t n_sources,
+                                        int64_t n_tokens, int64_t width,
+                                        const void* query, int64_t rank, float scale,
+                                        const void* out, const int8_t* out_refine,
+                                        const void* grad_out, const float* logit,
+                                        const float* inv_rms, const float* stats,
+                                        void* grad_values, void* grad_query, void* stream);
+
+/*
  * Source-list forward.  `sources` and `row_strides` are HOST arrays of
  * n_sources entries: source s, row n starts at sources[s] + n*row_strides[s].
  * Sources are never packed or copied.  Same outputs as the packed forward

@@ -293,3 +293,15 @@ def test_workspace_holds_the_widest_backward_grid():
     assert lib.attnres_hip_dq_workspace_elems(100, 1024, 1024) == (13 + 1) * 1024    # 8 groups of 32 lanes
     assert lib.attnres_hip_dq_workspace_elems(100, 8192, 8192) == (100 + 1) * 8192   # a workgroup per token
     assert lib.attnres_hip_dq_workspace_elems(10**6, 4096, 64) == (2048 + 1) * 64    # the persistent-grid cap
+
+
+def test_no_alloc_backward_checks_arguments_on_the_host():
+    """The no-allocation backward rejects bad shapes and null pointers before
+    any runtime call (so also on a machine without a GPU)."""
+    lib = _native.load()
+    args = [None, 0, 0, 2, 4, 64, None, 65, 1.0, None, None, None, None, None, None, None, None, None]
+    assert lib.attnres_hip_packed_backward_noalloc(*args) == _native.ERR_SHAPE
+    assert b"rank" in lib.attnres_hip_last_error()
+    args[7] = 64
+    assert lib.attnres_hip_packed_backward_noalloc(*args) == _native.ERR_NULL_POINTER
+    assert b"attnres_hip_packed_backward_noalloc" in lib.attnres_hip_last_error()
