@@ -5,7 +5,8 @@ Every token row is compared.  The oracle runs over token chunks
 independent, so a chunk's output and value-gradient rows are exactly the
 whole read's), and the query gradient is the chunks' unrounded gradients
 summed and rounded once.  Bars (tests/helpers.py): the BF16 gate against the
-BF16 oracle, one BF16 ulp against the float64 oracle, and the saved
+BF16 oracle, one BF16 ulp against the float64 oracle (value gradients of
+reads that save their output with the delta allowance), and the saved
 statistics within 1e-5 relative of the oracle's.
 
 * c1: the CPU plumbing configuration's exact inputs (packed [8, 2, 512, 1024],
@@ -31,7 +32,7 @@ import torch
 
 import bench
 from attnres import attnres
-from helpers import Streamed, check_statistics, compare, dv_floor, set_case
+from helpers import DELTA_SIGMAS, Streamed, check_statistics, compare, delta_allowance, saves_output, set_case
 from oracle.oracle import oracle_chunks
 
 pytestmark = pytest.mark.gpu
@@ -73,17 +74,28 @@ def _check_full(values, query, upstream, *, listed, chunk=2048, exact_all=True):
     out, dv, dq = _read(flat, query, g, listed)
     torch.cuda.synchronize()
     sources = len(values) if listed else int(values.shape[0])
-    out_check, dv_check = Streamed("out"), Streamed("dv", dv_floor(sources))
+    saved = saves_output(sources)
+    out_check, dv_check = Streamed("out"), Streamed("dv", allowance=saved)
     dq32 = dq64 = None
+    dq_variance = torch.zeros(int(query.numel()), dtype=torch.float64)
 
     def rows_of(start, stop, exact):
         return next(oracle_chunks(_rows(flat, listed, start, stop), query, g[start:stop], chunk=stop - start,
                                   exact=exact))
 
-    def add(start, stop, o, rows, o64=None, rows64=None):
+    def add(start, stop, o, rows, o64=None, rows64=None, whole=False):
+        """``whole``: a chunk of the pass over every token (its dq variance counts)."""
+        nonlocal dq_variance
         out_check.add(out[start:stop], o, o64)
+        extra = None
+        if saved and (rows64 is not None or whole):
+            packed = _stack([r.cpu() for r in _rows(flat, listed, start, stop)], True) if listed \
+                else flat[:, start:stop].cpu()
+            extra, variance = delta_allowance(packed.double(), query.cpu().double(), g[start:stop].cpu().double())
+            if whole:
+                dq_variance = dq_variance + variance
         dv_check.add(_stack(_rows(dv, listed, start, stop), listed), _stack(rows, listed),
-                     None if rows64 is None else _stack(rows64, listed))
+                     None if rows64 is None else _stack(rows64, listed), extra)
 
     for start in range(0, tokens, chunk):
         stop = min(tokens, start + chunk)
@@ -93,7 +105,7 @@ def _check_full(values, query, upstream, *, listed, chunk=2048, exact_all=True):
         if exact_all:
             _, _, o64, rows64, q64 = rows_of(start, stop, True)
             dq64 = q64 if dq64 is None else dq64 + q64
-        add(start, stop, o, rows, o64, rows64)
+        add(start, stop, o, rows, o64, rows64, whole=True)
     if not exact_all:
         for start in sorted({0, tokens // 2, max(0, tokens - 512)}):
             stop = min(tokens, start + 512)
@@ -102,7 +114,8 @@ def _check_full(values, query, upstream, *, listed, chunk=2048, exact_all=True):
             add(start, stop, o, rows, o64, rows64)
     out_check.finish()
     dv_check.finish()
-    metrics = compare(dq, dq32.to(torch.bfloat16), exact=dq64, name="dq")
+    dq_extra = DELTA_SIGMAS * dq_variance.sqrt() if saved else None
+    metrics = compare(dq, dq32.to(torch.bfloat16), exact=dq64, name="dq", extra=dq_extra)
     if dq64 is None:
         assert metrics["ulp_vs_oracle"] <= 1.0, f"dq: {metrics['ulp_vs_oracle']:.3f} ulps from the BF16 oracle"
     check_statistics(flat, query)
