@@ -159,8 +159,15 @@ def measured_traffic(config: str, key: str) -> int | None:
 
 
 def copy_probe(gib: float = 1.0, reps: int = 5) -> None:
-    """A plain device-to-device copy of known size (for counter scaling)."""
+    """Streams of known size, for scaling the FETCH_SIZE / WRITE_SIZE counters:
+    a device-to-device copy (torch), and the library's BF16 partial-sum kernel
+    (``attnres_partial_sum_kernel``: ``gib`` GiB read from two buffers and
+    ``gib`` GiB written to two, with the same non-temporal 16-byte loads and
+    stores as the read's kernels; the counters' scale depends on the access
+    width, so this one calibrates them)."""
     import torch
+
+    from attnres import _native
 
     elems = int(gib * 2**30) // 2
     src = torch.randn(elems, device="cuda").to(torch.bfloat16)
@@ -169,7 +176,18 @@ def copy_probe(gib: float = 1.0, reps: int = 5) -> None:
     for _ in range(reps):
         dst.copy_(src)
     torch.cuda.synchronize()
+    del dst
+    lib = _native.load()
+    half = elems // 2
+    prev, emitted = src[:half], src[half:2 * half]
+    out, out_bf16 = torch.empty_like(prev), torch.empty_like(prev)
+    stream = torch.cuda.current_stream().cuda_stream
+    for _ in range(reps):
+        _native.check(lib.attnres_hip_partial_sum(prev.data_ptr(), emitted.data_ptr(), 1, half, out.data_ptr(),
+                                                  out_bf16.data_ptr(), stream), "partial sum probe")
+    torch.cuda.synchronize()
     print(json.dumps({"copy_probe_bytes_read": elems * 2, "copy_probe_bytes_written": elems * 2,
+                      "partial_sum_probe_bytes_read": 4 * half, "partial_sum_probe_bytes_written": 4 * half,
                       "reps": reps}), flush=True)
 
 

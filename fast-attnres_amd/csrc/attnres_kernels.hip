@@ -120,9 +120,25 @@ __device__ __forceinline__ void load_row(const uint16_t* __restrict__ row, int l
   }
 }
 
-template <bool VEC>
+// Stores of rows whose base address is the same across the wavefront
+// (token groups of 64 lanes and more) are buffer stores with the sc1 and nt
+// cache bits: non-temporal, device scope.  The rows they write (outputs,
+// refinement bytes, value gradients) are read only by later kernels.
+// Measured on MI355X against the nt-only stores of __builtin_nontemporal_store:
+// c4 backward 503 -> 487 us, c3 backward 838 -> 829 us, c2 unchanged.
+// Narrower groups (several tokens per wavefront) keep the nt-only stores: a
+// buffer resource needs a wave-uniform base.
+constexpr int kStoreScNt = 16 | 2;  // cache policy: SC1 | NT
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_resource(const void* row, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(row), static_cast<short>(0), bytes, 0x00020000);
+}
+
+template <int G, bool VEC>
 __device__ __forceinline__ void store_chunk(uint16_t* __restrict__ row, int d0, int D, const u32x4& w) {
-  if constexpr (VEC) {
+  if constexpr (VEC && G >= 64) {
+    __builtin_amdgcn_raw_buffer_store_b128(w, row_resource(row, 2 * D), 2 * d0, 0, kStoreScNt);
+  } else if constexpr (VEC) {
     __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(row + d0));
   } else {
     const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
@@ -173,8 +189,10 @@ __device__ __forceinline__ void store_row_refined(uint16_t* __restrict__ row, in
         r[j >> 1] |= (q0 | (q1 << 8)) << (16 * (j & 1));
       }
     }
-    store_chunk<VEC>(row, d0, D, u32x4{w[0], w[1], w[2], w[3]});
+    store_chunk<G, VEC>(row, d0, D, u32x4{w[0], w[1], w[2], w[3]});
     if constexpr (!REFINE) {
+    } else if constexpr (VEC && G >= 64) {
+      __builtin_amdgcn_raw_buffer_store_b64(u32x2{r[0], r[1]}, row_resource(refine, D), d0, 0, kStoreScNt);
     } else if constexpr (VEC) {
       __builtin_nontemporal_store(u32x2{r[0], r[1]}, reinterpret_cast<u32x2*>(refine + d0));
     } else {
@@ -875,7 +893,7 @@ __global__ void __launch_bounds__(kBlock) attnres_bwd_kernel(const BwdArgs<Rows,
             }
           }
         } else if (NOMASK || d0 < D) {
-          store_chunk<VEC>(grad_row, d0, D, u32x4{out[0], out[1], out[2], out[3]});
+          store_chunk<G, VEC>(grad_row, d0, D, u32x4{out[0], out[1], out[2], out[3]});
         }
       }
       }  // kCoef
@@ -1019,7 +1037,7 @@ __global__ void __launch_bounds__(kBlock) attnres_bwd_recompute_kernel(const Bwd
           dq[c][2 * k + 1] = fmaf(ca, k1, dq[c][2 * k + 1]);
           out[k] = pack_bf16x2(v0, v1);
         }
-        if (NOMASK || d0 < D) store_chunk<VEC>(grad_row, d0, D, u32x4{out[0], out[1], out[2], out[3]});
+        if (NOMASK || d0 < D) store_chunk<G, VEC>(grad_row, d0, D, u32x4{out[0], out[1], out[2], out[3]});
       }
     }
   }
@@ -1129,7 +1147,7 @@ __global__ void __launch_bounds__(kBlock) attnres_gather_kernel(const GatherArgs
           uint16_t* grad_row = static_cast<uint16_t*>(a.grad) + tok[t] * D;
           const u32x4 packed{pack_bf16x2(acc[t][c][0], acc[t][c][1]), pack_bf16x2(acc[t][c][2], acc[t][c][3]),
                              pack_bf16x2(acc[t][c][4], acc[t][c][5]), pack_bf16x2(acc[t][c][6], acc[t][c][7])};
-          if (d0 < D) store_chunk<VEC>(grad_row, d0, D, packed);
+          if (d0 < D) store_chunk<G, VEC>(grad_row, d0, D, packed);
           continue;
         }
         float* grad_row = static_cast<float*>(a.grad) + tok[t] * D;
