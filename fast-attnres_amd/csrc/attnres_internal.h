@@ -201,10 +201,11 @@ inline bool no_mask(const Geometry& geo, int64_t width, int64_t rank) {
 // per token with 2 chunks per lane; every other geometry keeps its group.
 constexpr int recompute_lanes(int lanes, int chunks) { return lanes == 64 && chunks == 8 ? kBlock : lanes; }
 
-// Persistent grid for N tokens in groups of `group_lanes` lanes: one group
-// per token at most, capped by the workgroups that stay resident on the
-// device (`resident` <= 0: unknown), by kMaxGridBlocks and by `cap` (<= 0:
-// none; the dq partial rows the caller's buffer holds).
+// Grid for N tokens in groups of `group_lanes` lanes whose groups stride over
+// the tokens: one group per token at most, capped by `resident` (the
+// workgroups that stay resident on the device, or a multiple of them; <= 0:
+// unknown), by kMaxGridBlocks and by `cap` (<= 0: none; the dq partial rows
+// the caller's buffer holds).
 inline int64_t grid_blocks(int64_t N, int group_lanes, int64_t resident, int64_t cap = 0) {
   const int64_t groups = kBlock / group_lanes;
   int64_t blocks = (N + groups - 1) / groups;

@@ -25,9 +25,9 @@
 // of the full row) is updated; the per-source logit and 1/rms and the
 // per-token (max, 1/sum) are saved for the backward.
 //
-// Backward.  A persistent grid; group g takes tokens g, g + groups, ... so
-// that the groups work on neighbouring tokens at any time and walk the
-// sources roughly in step.  The ring of value rows crosses token boundaries;
+// Backward.  A grid of up to four resident grids; group g takes tokens g,
+// g + groups, ... so that the groups work on neighbouring tokens at any time
+// and walk the sources roughly in step.  The ring of value rows crosses token boundaries;
 // at each new token the group loads dO and the saved output (BF16 plus one
 // refinement byte per element, see refine_encode) and forms
 // delta = <dO, o>.  Per item: dw = <v, dO>, p = exp(z - max) / sum,
@@ -1274,10 +1274,18 @@ void launch_fwd_geometry(const FwdArgs<Rows>& a, bool nomask, bool vec, hipStrea
   }
 }
 
+// The streaming backward's grid: up to four times the workgroups that fit
+// on the device at once.  Its token shares are static, so with one resident
+// grid the slowest workgroup sets the kernel's end; with more, shorter
+// workgroups the hardware hands the later ones to whichever CU frees up
+// first.  Measured on MI355X (backward, us, one resident grid -> four):
+// c2 629 -> 622, c3 833 -> 830, c4 496 -> 488.
+constexpr int64_t kBwdGridPerResident = 4;
+
 template <int G, int CH, int NB, bool NOMASK, bool VEC, bool ACC, class Rows, class Grads>
 int64_t launch_bwd_ring(const BwdArgs<Rows, Grads>& a, hipStream_t stream) {
   const int64_t resident = resident_blocks<&attnres_bwd_kernel<G, CH, NB, NOMASK, VEC, ACC, Rows, Grads>>();
-  const int64_t blocks = grid_blocks(a.n_tokens, G, resident, a.max_grid);
+  const int64_t blocks = grid_blocks(a.n_tokens, G, kBwdGridPerResident * resident, a.max_grid);
   hipLaunchKernelGGL((attnres_bwd_kernel<G, CH, NB, NOMASK, VEC, ACC, Rows, Grads>),
                      dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream, a);
   return blocks;
