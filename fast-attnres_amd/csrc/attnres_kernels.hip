@@ -25,7 +25,7 @@
 // of the full row) is updated; the per-source logit and 1/rms and the
 // per-token (max, 1/sum) are saved for the backward.
 //
-// Backward.  A grid of up to four resident grids; group g takes tokens g,
+// Backward.  A grid of up to two resident grids; group g takes tokens g,
 // g + groups, ... so that the groups work on neighbouring tokens at any time
 // and walk the sources roughly in step.  The ring of value rows crosses token boundaries;
 // at each new token the group loads dO and the saved output (BF16 plus one
@@ -1274,13 +1274,16 @@ void launch_fwd_geometry(const FwdArgs<Rows>& a, bool nomask, bool vec, hipStrea
   }
 }
 
-// The streaming backward's grid: up to four times the workgroups that fit
-// on the device at once.  Its token shares are static, so with one resident
-// grid the slowest workgroup sets the kernel's end; with more, shorter
-// workgroups the hardware hands the later ones to whichever CU frees up
-// first.  Measured on MI355X (backward, us, one resident grid -> four):
-// c2 629 -> 622, c3 833 -> 830, c4 496 -> 488.
-constexpr int64_t kBwdGridPerResident = 4;
+// The streaming backward's grid: up to two times the workgroups that fit on
+// the device at once.  Its token shares are static, so with one resident
+// grid the slowest workgroup sets the kernel's end (per-launch durations at
+// c2 ranged 578-708 us on one box); with more, shorter workgroups the
+// hardware hands the later ones to whichever CU frees up first.  Each
+// workgroup also writes one dq partial row, which the reduction reads.
+// Measured on MI355X (backward op, us): one resident grid -> two: c2 629 ->
+// 617-624, c3 833 -> 827-829; two -> four on another box: c2 618 -> 627, c3
+// 824 -> 826, c4 481 -> 486 (four: 2048 partial rows, a reduction of 11 us).
+constexpr int64_t kBwdGridPerResident = 2;
 
 template <int G, int CH, int NB, bool NOMASK, bool VEC, bool ACC, class Rows, class Grads>
 int64_t launch_bwd_ring(const BwdArgs<Rows, Grads>& a, hipStream_t stream) {
