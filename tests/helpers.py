@@ -198,6 +198,8 @@ def compare(actual: torch.Tensor, expected: torch.Tensor, *, tol=BF16_TOLERANCE,
                "allowance": extra is not None}
     if exact is not None:
         metrics["ulp_vs_float64"] = ulp_error(actual, exact, floor, extra)
+        if extra is not None:
+            metrics["ulp_vs_float64_floor_only"] = ulp_error(actual, exact, floor)
     RECORDS.append(metrics)
     if exact is not None and ulps is not None:
         assert metrics["ulp_vs_float64"] <= ulps, (
@@ -220,6 +222,7 @@ class Streamed:
         self.diff_sq = 0.0
         self.ref_sq = 0.0
         self.ulp_exact = None
+        self.ulp_floor_only = 0.0
         self.worst = ""
 
     def add(self, actual: torch.Tensor, expected: torch.Tensor, exact: torch.Tensor | None = None,
@@ -243,6 +246,8 @@ class Streamed:
             if ulps > (self.ulp_exact or 0.0):
                 self.worst = worst_element(actual, exact, self.floor, extra, excess)
             self.ulp_exact = max(self.ulp_exact or 0.0, ulps)
+            if extra is not None:
+                self.ulp_floor_only = max(self.ulp_floor_only, ulp_error(actual, exact, self.floor))
 
     def finish(self, ulps: float | None = 1.0) -> dict:
         metrics = {"case": _CASE[0], "tensor": self.name, "max_abs": self.max_abs,
@@ -250,6 +255,8 @@ class Streamed:
                    "floor": self.floor, "allowance": self.allowance}
         if self.ulp_exact is not None:
             metrics["ulp_vs_float64"] = self.ulp_exact
+            if self.allowance:
+                metrics["ulp_vs_float64_floor_only"] = self.ulp_floor_only
         RECORDS.append(metrics)
         if self.ulp_exact is not None and ulps is not None:
             assert self.ulp_exact <= ulps, (f"{self.name}: {self.ulp_exact:.3f} BF16 ulps from the float64 oracle "
