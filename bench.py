@@ -34,7 +34,10 @@ gradient accumulation over the reads (what autograd adds for shared
 sources) is timed separately from the operator.  ``c5`` is the 24-layer
 Full-schedule sweep: one packed read for each S = 1..48 at N=16384, for
 D in {1024, 4096} and R in {D, D/4}; a step is the 48 reads of one (D, R)
-and the line reports the summed operator time per step.
+and the line reports the summed operator time per step (each read timed on
+its own, one autograd.grad call per read), plus ``one_backward_pass``: the
+same reads as a training step runs them, every forward and then one
+autograd.backward over all the outputs.
 
 ``model`` is the caller: one training step (forward, backward, AdamW) of the
 24-layer Full-schedule causal LM of ``benchmarks/model.py`` at D=1024 on
@@ -48,8 +51,10 @@ The c2..c3 lines also carry ``graph_replay``: the forward, the backward and
 the whole read through the C ABI captured into HIP graphs and replayed (the
 kernels' time without host or launch gaps), median and quartiles over rounds.
 
-``--copy-probe`` runs only a plain device copy of known size, used to scale
-the hardware FETCH_SIZE / WRITE_SIZE counters when profiling.
+``--copy-probe`` runs only streams of known size (a device copy, and the
+library's partial-sum kernel, whose non-temporal 16-byte accesses match the
+read's kernels), used to scale the hardware FETCH_SIZE / WRITE_SIZE counters
+when profiling.
 """
 
 from __future__ import annotations
@@ -463,6 +468,33 @@ def run_block_schedule(cfg: dict, steps: int, warmup: int, cpu_budget: float | N
     }
 
 
+def _sweep_one_backward_pass(values, query, grad_out, max_sources: int, steps: int, warmup: int) -> float:
+    """ms for the 48 reads of one (D, R) as a training step runs them: every
+    forward, then one ``torch.autograd.backward`` over all the outputs (one
+    autograd engine call per step instead of one per read; each read has
+    its own value and query leaves, so no gradient is accumulated)."""
+    import torch
+
+    from attnres import attnres
+
+    def step():
+        leaves = [values[:s].detach().requires_grad_() for s in range(1, max_sources + 1)]
+        queries = [query.detach().requires_grad_() for _ in leaves]
+        outs = [attnres(leaf, q) for leaf, q in zip(leaves, queries)]
+        torch.autograd.backward(outs, [grad_out] * len(outs))
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    start, stop = _event(), _event()
+    start.record()
+    for _ in range(steps):
+        step()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps
+
+
 def run_sweep(cfg: dict, steps: int, warmup: int) -> dict:
     """c5: one packed read per S = 1..48 (N=16384) for each D and R in
     {D, D/4}; the value rows of a read are the first S sources of one
@@ -501,10 +533,13 @@ def run_sweep(cfg: dict, steps: int, warmup: int) -> dict:
                 per_read.append([sources, round(ms * 1e3, 2), round((fwd_bytes + bwd_bytes) / (ms * 1e-3) / 1e12, 4)])
                 step_ms += ms
                 step_bytes += fwd_bytes + bwd_bytes
+            one_pass_ms = _sweep_one_backward_pass(values, query, grad_out, max_sources, steps, warmup)
             del values, grad_out
             torch.cuda.empty_cache()
             sweep.append({"width": width, "rank": rank, "ms_per_step": round(step_ms, 4),
                           "TB/s": round(step_bytes / (step_ms * 1e-3) / 1e12, 4),
+                          "one_backward_pass": {"ms_per_step": round(one_pass_ms, 4),
+                                                "TB/s": round(step_bytes / (one_pass_ms * 1e-3) / 1e12, 4)},
                           "bytes_per_step": step_bytes, "per_read_S_us_TBs": per_read})
             total_bytes += step_bytes
             total_ms += step_ms
@@ -516,9 +551,19 @@ def run_sweep(cfg: dict, steps: int, warmup: int) -> dict:
         "pct_of_peak": round(100 * value / HBM_PEAK_TBS, 2), "vs_baseline": None, "dtype": "f32",
         "storage_dtype": "bf16", "data": "synthetic (seeded; per-source std U[0.5,4], 1% channels x8)",
         "config": {"workload": cfg["name"], "tokens": tokens, "layout": "packed",
-                   "note": "ms_per_step is the mean over the four (D, R) steps; each step's own time is in sweep"},
+                   "note": "ms_per_step is the mean over the four (D, R) steps; each step's own time is in sweep "
+                           "(reads timed one by one, one autograd.grad call each); one_backward_pass: the same "
+                           "48 reads with all forwards, then one autograd.backward"},
+        "one_backward_pass": {"ms_per_step": round(sum(x["one_backward_pass"]["ms_per_step"] for x in sweep)
+                                                   / len(sweep), 4),
+                              "TB/s": round(total_bytes / (sum(x["one_backward_pass"]["ms_per_step"] for x in sweep)
+                                                           * 1e-3) / 1e12, 4)},
         "sweep": sweep,
-        "roofline": None,
+        # the sweep's reads as a whole (event-timed forward + backward ops; the D = 4096
+        # backward kernels take about half of the traced time): algorithmic bytes / time
+        "roofline": {"bound": "hbm", "kernel": "every read of the sweep: forward + backward ops",
+                     "achieved": round(value * 1e3, 1), "peak": HBM_PEAK_TBS * 1e3, "unit": "GB/s",
+                     "frac": round(value / HBM_PEAK_TBS, 4), "traffic": None},
         "cpu_baseline": None,
     }
 
