@@ -927,6 +927,194 @@ __global__ void __launch_bounds__(kBlock) attnres_bwd_kernel(const BwdArgs<Rows,
   store_dq_partial<G, CH>(dq, dq_lds, a.partial + static_cast<int64_t>(blockIdx.x) * R, group, lane, tail0, D);
 }
 
+// ---------------------------------------------------- backward, token blocks
+
+// Token-block backward for 64-lane rows of 4 chunks (D = 2048, R = D): a
+// group owns T consecutive tokens at a time (blocks b, b + groups, ... of a
+// persistent grid) and walks their items source-major, (s, 0), (s, 1), ...,
+// (s, T-1), (s + 1, 0), ...  Ring slot t serves token t, so the value rows a
+// group has in flight, and the dv rows it stores one after another, are one
+// source's rows of adjacent tokens: a contiguous span.  The streaming kernel
+// instead keeps consecutive sources of one token in flight, rows a source
+// stride apart, and how fast those move depends on where the buffers lie in
+// physical memory: at c2 the streaming backward takes 602-660 us depending on
+// the placement of values and gradients, this kernel 590-610 us under every
+// placement measured.  Per-token arithmetic is the streaming kernel's (same
+// sums in the same order), so the results are bit-identical.
+//
+// The next block's dO, output, refinement bytes and statistics are requested
+// two sources before the block ends and folded into delta after its last
+// item; slots wrap into the next block without draining.  With T = 4 the
+// kernel needs more than 256 registers (AGPRs hold the rest) and runs one
+// wave per SIMD: four rows in flight per wave.  T = 2 and 3 were slower
+// (680 and 700 us at c2).  It is launched with NOMASK only (the masked
+// instances spill).  Its timing is sensitive to code generation: a version
+// with a few equivalent source edits (a named request step, a hoisted idle
+// row) compiled to a kernel that took 670 us instead of 590 us at c2, so
+// changes here are measured before they are kept.
+template <int G, int CH, int T, bool NOMASK, bool VEC, class Rows, class Grads>
+__global__ void __launch_bounds__(kBlock) attnres_bwd_block_kernel(const BwdArgs<Rows, Grads> a) {
+  static_assert(G == 64, "one wavefront per token");
+  static_assert(std::is_same_v<Grads, PackedGrads> || std::is_same_v<Grads, ListGrads>, "BF16 dv rows");
+  constexpr int kGroups = kBlock / G;
+  __shared__ float xred[1];
+  __shared__ float dq_lds[kGroups * G * kVec];
+  __shared__ __attribute__((aligned(16))) float q_lds[G * CH * kVec];
+  const int lane = threadIdx.x % G;
+  const int group = group_index<G>();
+  const int D = a.width;
+  const int R = a.rank;
+  const int tail0 = D - R;
+  const int S = a.n_sources;
+  const int64_t N = a.n_tokens;
+  const float inv_R = 1.0f / static_cast<float>(R);
+  const float scale = a.scale;
+  int phase = 0;
+
+  fill_query_lds<G, CH>(a.query, q_lds, tail0, D, R);
+  uint32_t km[CH][4];
+  if constexpr (!NOMASK) key_masks<G, CH>(lane, D, tail0, km);
+  float dq[CH][kVec];
+#pragma unroll
+  for (int c = 0; c < CH; ++c)
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) dq[c][e] = 0.0f;
+
+  const int64_t n_blocks = (N + T - 1) / T;
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * kGroups + group;
+  const int64_t groups = static_cast<int64_t>(gridDim.x) * kGroups;
+  const int64_t my_blocks = gid < n_blocks ? (n_blocks - 1 - gid) / groups + 1 : 0;
+
+  if (my_blocks > 0) {
+    // tokens of block b (clamped: a token past N repeats token N-1 and stores nothing)
+    auto token_of = [&](int64_t b, int t) __attribute__((always_inline)) {
+      const int64_t n = b * T + t;
+      return n < N ? n : N - 1;
+    };
+    int64_t blk = gid;
+    const int64_t last_blk = gid + (my_blocks - 1) * groups;
+    u32x4 g[T][CH];
+    float delta[T], run_max[T], inv_sum[T];
+    TokenRows<CH> pend[T];
+    auto request = [&](int64_t b) __attribute__((always_inline)) {
+#pragma unroll
+      for (int t = 0; t < T; ++t) load_token<G, CH, VEC>(a, token_of(b, t), lane, pend[t]);
+    };
+    auto fold = [&]() __attribute__((always_inline)) {
+      float red[T];
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        if constexpr (!NOMASK) mask_range<G, CH>(lane, D, pend[t].g);
+        red[t] = token_delta<CH>(pend[t]);
+      }
+      group_sum<G, T>(red, xred, phase);
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        delta[t] = red[t];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) g[t][c] = pend[t].g[c];
+        run_max[t] = pend[t].run_max;
+        inv_sum[t] = pend[t].inv_sum;
+      }
+    };
+    request(blk);
+    fold();
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ring slot t: the next row of token t of the current (or next) block
+    u32x4 ring[T][CH];
+    float ring_z[T], ring_r[T];
+    auto refill = [&](int t, int s, int64_t b, bool live) __attribute__((always_inline)) {
+      const int64_t n = token_of(b, t);
+      const uint16_t* row = live ? a.src.row(s, n) : a.src.row(0, token_of(blk, 0));
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const int d0 = chunk_start<G>(c, lane);
+        const int offset = (live && d0 < D) ? d0 : 0;
+        if constexpr (VEC) {
+          ring[t][c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(row + offset));
+        }
+      }
+      if constexpr (!VEC) load_row<G, CH, VEC>(row, lane, D, ring[t]);
+      const int64_t item = live ? n * S + s : 0;
+      ring_z[t] = a.logit[item];
+      ring_r[t] = a.inv_rms[item];
+    };
+#pragma unroll
+    for (int t = 0; t < T; ++t) refill(t, 0, blk, true);
+
+    int s = 0;
+    for (;;) {
+      // next row of every slot: source s + 1 of this block, or source 0 of the next block
+      const bool wrap = s + 1 == S;
+      const int64_t nb = wrap ? blk + groups : blk;
+      const bool live_next = !wrap || blk < last_blk;
+      if (s == S - 2 && blk < last_blk) request(blk + groups);
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const int64_t token = token_of(blk, t);
+        const bool valid = blk * T + t < N;
+        float dw[1] = {0.0f};
+        {
+          float dw1 = 0.0f;
+#pragma unroll
+          for (int c = 0; c < CH; ++c) {
+            dw[0] = dot2(ring[t][c].x, g[t][c].x, dw[0]);
+            dw1 = dot2(ring[t][c].y, g[t][c].y, dw1);
+            dw[0] = dot2(ring[t][c].z, g[t][c].z, dw[0]);
+            dw1 = dot2(ring[t][c].w, g[t][c].w, dw1);
+          }
+          dw[0] += dw1;
+        }
+        group_sum<G, 1>(dw, xred, phase);
+        const float z = ring_z[t];
+        const float inv_rms = ring_r[t];
+        const float p = __expf(z - run_max[t]) * inv_sum[t];
+        const float dz = valid ? p * (dw[0] - delta[t]) : 0.0f;
+        const float ca = inv_rms * (dz * scale);
+        const float cb = -(inv_rms * inv_rms) * (dz * z * inv_R);
+        auto* grad_row = a.grad.row(s, token, D);
+        const uint32_t lo_shift = 16u | (static_cast<uint32_t>(s) >> 31);
+        const uint32_t hi_mask = 0xffff0000u | (static_cast<uint32_t>(s) >> 31);
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+          const int d0 = chunk_start<G>(c, lane);
+          const uint32_t w[4] = {ring[t][c].x, ring[t][c].y, ring[t][c].z, ring[t][c].w};
+          const uint32_t gw[4] = {g[t][c].x, g[t][c].y, g[t][c].z, g[t][c].w};
+          const float4 qa = *reinterpret_cast<const float4*>(&q_lds[d0]);
+          const float4 qb = *reinterpret_cast<const float4*>(&q_lds[d0 + 4]);
+          const float qf[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+          uint32_t out[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const uint32_t kw = NOMASK ? w[k] : (w[k] & km[c][k]);
+            const float k0 = bf16_lo(kw), k1 = bf16_hi(kw);
+            const float g0 = __uint_as_float(gw[k] << lo_shift), g1 = __uint_as_float(gw[k] & hi_mask);
+            const float v0 = fmaf(cb, k0, fmaf(ca, qf[2 * k], p * g0));
+            const float v1 = fmaf(cb, k1, fmaf(ca, qf[2 * k + 1], p * g1));
+            dq[c][2 * k] = fmaf(ca, k0, dq[c][2 * k]);
+            dq[c][2 * k + 1] = fmaf(ca, k1, dq[c][2 * k + 1]);
+            out[k] = pack_bf16x2(v0, v1);
+          }
+          if (valid && (NOMASK || d0 < D)) store_chunk<G, VEC>(grad_row, d0, D, u32x4{out[0], out[1], out[2], out[3]});
+        }
+        __builtin_amdgcn_sched_barrier(0);  // refill the slot after its last use
+        refill(t, wrap ? 0 : s + 1, nb, live_next);
+      }
+      if (wrap) {
+        if (blk == last_blk) break;
+        fold();
+        blk += groups;
+        s = 0;
+      } else {
+        ++s;
+      }
+    }
+  }
+
+  store_dq_partial<G, CH>(dq, dq_lds, a.partial + static_cast<int64_t>(blockIdx.x) * R, group, lane, tail0, D);
+}
+
 // ------------------------------------------------ backward, recompute policy
 
 // For S <= kRecomputeMaxSources the forward stores no refinement and this
@@ -1294,8 +1482,30 @@ int64_t launch_bwd_ring(const BwdArgs<Rows, Grads>& a, hipStream_t stream) {
   return blocks;
 }
 
+// The token-block backward (attnres_bwd_block_kernel) takes the plain
+// backward of aligned, unmasked rows of 2048 elements (R = D) with BF16
+// gradient rows, packed or list, T = 4 tokens per group, for reads of at
+// least kBwdBlockMinSources sources.
+template <int G, int CH, bool NOMASK, bool VEC, bool ACC, class Grads>
+constexpr bool kBwdBlockVariant = G == 64 && CH == 4 && NOMASK && VEC && !ACC &&
+                                  (std::is_same_v<Grads, PackedGrads> || std::is_same_v<Grads, ListGrads>);
+constexpr int kBwdBlockTokens = 4;
+constexpr int kBwdBlockMinSources = 2;
+
+template <int G, int CH, int T, bool VEC, class Rows, class Grads>
+int64_t launch_bwd_block(const BwdArgs<Rows, Grads>& a, hipStream_t stream) {
+  const int64_t resident = resident_blocks<&attnres_bwd_block_kernel<G, CH, T, true, VEC, Rows, Grads>>();
+  const int64_t blocks = grid_blocks((a.n_tokens + T - 1) / T, G, kBwdGridPerResident * resident, a.max_grid);
+  hipLaunchKernelGGL((attnres_bwd_block_kernel<G, CH, T, true, VEC, Rows, Grads>), dim3(static_cast<unsigned>(blocks)),
+                     dim3(kBlock), 0, stream, a);
+  return blocks;
+}
+
 template <int G, int CH, bool NOMASK, bool VEC, bool ACC, class Rows, class Grads>
 int64_t launch_bwd(const BwdArgs<Rows, Grads>& a, hipStream_t stream) {
+  if constexpr (kBwdBlockVariant<G, CH, NOMASK, VEC, ACC, Grads>) {
+    if (a.n_sources >= kBwdBlockMinSources) return launch_bwd_block<G, CH, kBwdBlockTokens, VEC>(a, stream);
+  }
   if constexpr (kBwdTwoRowVariant<CH, VEC, ACC> && G >= 64) {
     return launch_bwd_ring<G, CH, 2, NOMASK, VEC, ACC>(a, stream);
   } else if constexpr (kBwdTwoRowVariant<CH, VEC, ACC>) {

@@ -97,6 +97,33 @@ def test_aligned_fast_path_matches_oracle(width, rank, layout):
 
 
 @pytest.mark.parametrize("layout", ["packed", "list"])
+@pytest.mark.parametrize("sources,tokens", [(7, 1), (7, 3), (8, 4097), (13, 1030), (25, 2049)],
+                         ids=lambda v: str(v))
+def test_token_block_backward_matches_oracle(sources, tokens, layout):
+    """Aligned, unmasked rows of 2048 elements (R = D) take the token-block
+    backward, four tokens per group: a single token, token counts that are not
+    a multiple of four (the last block repeats a token and stores nothing for
+    it), grids of few and of many blocks."""
+    torch.manual_seed(SEEDS[1] + sources * tokens)
+    width = rank = 2048
+    values = torch.randn(sources, tokens, width, device="cuda", dtype=torch.bfloat16)
+    values = (values * torch.linspace(0.5, 4, sources, device="cuda", dtype=torch.bfloat16)[:, None, None])
+    values.requires_grad_()
+    query = (torch.randn(rank, device="cuda", dtype=torch.bfloat16) / math.sqrt(rank)).requires_grad_()
+    upstream = torch.randn(tokens, width, device="cuda", dtype=torch.bfloat16)
+
+    def make(leaves, q):
+        return (tuple(leaves[0].unbind(0)) if layout == "list" else leaves[0]), q
+
+    print(f"token blocks S={sources} N={tokens} layout={layout}", flush=True)
+    set_case(f"token blocks S={sources} N={tokens} {layout}")
+    actual = attnres(make([values], query)[0], query)
+    grads = torch.autograd.grad(actual, (values, query), upstream)
+    expected, exact = both_oracles(make, [values], query, upstream)
+    compare_read((actual, *grads), expected, exact, ["out", "dv", "dq"], sources=sources)
+
+
+@pytest.mark.parametrize("layout", ["packed", "list"])
 @pytest.mark.parametrize("tokens,width,rank", [(2048, 1024, 1024), (4096, 1024, 1024), (4096, 1024, 256),
                                                (2048, 1024, 256), (3000, 2048, 512), (64, 8192, 8192)],
                          ids=lambda v: str(v))

@@ -19,7 +19,7 @@ import pytest
 import torch
 
 from attnres import SharedSources, attnres
-from helpers import compare
+from helpers import compare, ulp_error
 from oracle.oracle import oracle
 
 pytestmark = pytest.mark.gpu
@@ -54,8 +54,10 @@ def test_shared_sources_match_autograd_sums_and_the_oracle(width, rank):
     count = len(src)
     for a, b in zip(outs_bank, outs_ref):
         assert torch.equal(a, b)
-    for a, b in zip(grads_bank[count:], grads_ref[count:]):  # dq: same kernels, same order
-        assert torch.equal(a, b)
+    for a, b in zip(grads_bank[count:], grads_ref[count:]):
+        # dq: the same terms summed in the order of each kernel's grid; at D = 2048, R = D the
+        # plain read runs the token-block backward, whose grid differs from the accumulating one
+        assert ulp_error(a, b.double()) <= 1.0
     for a, b in zip(grads_bank[:count], grads_ref[:count]):
         # two BF16 roundings of partial sums apart at most, on the scale of the gradient
         torch.testing.assert_close(a.float(), b.float(), rtol=2.0**-6, atol=2.0**-6 * float(b.float().abs().max()))
