@@ -906,7 +906,8 @@ def main(argv=None) -> int:
         "backward": {"us": round(bwd_avg * 1e3, 2), "bytes": bwd_bytes, "TB/s": round(bwd_tbs, 4),
                      "pct_of_peak": round(100 * bwd_tbs / HBM_PEAK_TBS, 2)},
         "roofline": {"bound": "hbm",
-                     "kernel": "backward op: attnres_bwd_kernel + attnres_dq_reduce_kernel",
+                     "kernel": ("backward op: " + ("attnres_bwd_block_kernel" if sources >= 13 and width == cfg["rank"] == 2048
+                                                  else "attnres_bwd_kernel") + " + attnres_dq_reduce_kernel"),
                      "achieved": round(bwd_tbs * 1e3, 1), "peak": HBM_PEAK_TBS * 1e3,
                      "unit": "GB/s", "frac": round(bwd_tbs / HBM_PEAK_TBS, 4),
                      "traffic": measured_traffic(args.config, "backward_bytes")},

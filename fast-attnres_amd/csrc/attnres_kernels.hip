@@ -1485,12 +1485,17 @@ int64_t launch_bwd_ring(const BwdArgs<Rows, Grads>& a, hipStream_t stream) {
 // The token-block backward (attnres_bwd_block_kernel) takes the plain
 // backward of aligned, unmasked rows of 2048 elements (R = D) with BF16
 // gradient rows, packed or list, T = 4 tokens per group, for reads of at
-// least kBwdBlockMinSources sources.
+// least kBwdBlockMinSources sources.  Measured on MI355X (backward alone,
+// us, streaming -> token blocks): S = 25, N = 16384: 602-670 -> 590-600;
+// S = 13, N = 32768: 706-714 -> 656-668; S = 49, N = 8192: 610-635 -> 565;
+// but S = 12, N = 16384: 309-312 -> 315; S = 9, N = 32768: 479-487 ->
+// 501-516; S = 7: 390 -> 397-402 (fewer sources per block leave less to
+// stream between the block switches).
 template <int G, int CH, bool NOMASK, bool VEC, bool ACC, class Grads>
 constexpr bool kBwdBlockVariant = G == 64 && CH == 4 && NOMASK && VEC && !ACC &&
                                   (std::is_same_v<Grads, PackedGrads> || std::is_same_v<Grads, ListGrads>);
 constexpr int kBwdBlockTokens = 4;
-constexpr int kBwdBlockMinSources = 2;
+constexpr int kBwdBlockMinSources = 13;
 
 template <int G, int CH, int T, bool VEC, class Rows, class Grads>
 int64_t launch_bwd_block(const BwdArgs<Rows, Grads>& a, hipStream_t stream) {
