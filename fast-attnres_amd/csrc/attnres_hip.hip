@@ -343,7 +343,7 @@ using namespace attnres_hip;
 
 extern "C" {
 
-const char* attnres_hip_version(void) { return "2.0.0"; }
+const char* attnres_hip_version(void) { return "2.0.1+mi355x.1"; }
 
 const char* attnres_hip_last_error(void) { return g_error; }
 

@@ -77,7 +77,7 @@ enum attnres_status {
 /* Reads one attnres_hip_bank_gather launch takes (more take further launches). */
 #define ATTNRES_MAX_GATHER_READS 48
 
-/* Library version string, e.g. "1.0.0". */
+/* Library version string; the Python package's __version__ (e.g. "2.0.1+mi355x.1"). */
 const char* attnres_hip_version(void);
 
 /* Message for the calling thread's most recent non-OK status. */

@@ -55,7 +55,9 @@ def test_library_loads_and_exports_every_symbol():
     lib = _native.load()
     for name in _declarations():
         assert hasattr(lib, name), name
-    assert lib.attnres_hip_version().decode()
+    import attnres
+
+    assert lib.attnres_hip_version().decode() == attnres.__version__
 
 
 def test_workspace_size_is_shape_only_and_rejects_bad_shapes():
