@@ -97,13 +97,13 @@ def test_aligned_fast_path_matches_oracle(width, rank, layout):
 
 
 @pytest.mark.parametrize("layout", ["packed", "list"])
-@pytest.mark.parametrize("sources,tokens", [(13, 1), (13, 3), (14, 4097), (16, 1030), (25, 2049)],
+@pytest.mark.parametrize("sources,tokens", [(13, 1), (13, 3), (14, 4097), (16, 1030), (25, 2049), (49, 130), (129, 37)],
                          ids=lambda v: str(v))
 def test_token_block_backward_matches_oracle(sources, tokens, layout):
     """Aligned, unmasked rows of 2048 elements (R = D) of at least 13 sources
     take the token-block backward, four tokens per group: a single token, token counts that are not
     a multiple of four (the last block repeats a token and stores nothing for
-    it), grids of few and of many blocks."""
+    it), grids of few and of many blocks, up to the envelope's 129 sources."""
     torch.manual_seed(SEEDS[1] + sources * tokens)
     width = rank = 2048
     values = torch.randn(sources, tokens, width, device="cuda", dtype=torch.bfloat16)
