@@ -539,6 +539,185 @@ __global__ void __launch_bounds__(kBlock) attnres_fwd_kernel(const FwdArgs<Rows>
   }
 }
 
+// Token-block forward: a group owns T consecutive tokens and streams their
+// rows source-major -- items (s, t) for s = 0..S-1, t = 0..T-1 -- through a
+// ring of T * NBT slots; slot j always serves token j % T.  The rows a group
+// has in flight are then one source's rows of adjacent tokens (a contiguous
+// span) rather than several sources of one token, rows a power-of-two source
+// stride apart that can fall into the same DRAM banks.  Per-token arithmetic
+// is the one-token kernel's (same sums in the same order): bit-identical
+// results.  Used with T = 2, NBT = 2 (four rows in flight, two per token,
+// 206 VGPRs, two waves per SIMD) for 5 <= S <= 12 at D = R = 2048; see
+// launch_fwd for the measurements.  QLDS (query words from LDS) and WPE
+// (waves per SIMD the compiler must fit) were measured variants and are not
+// used (T = 4 at two waves per SIMD: 317-349 against 299-323 us at c2).
+// Like the token-block backward, its timing is sensitive to code generation:
+// changes are measured before they are kept.
+template <int G, int CH, int T, int NBT, bool NOMASK, bool VEC, class Rows, bool QLDS = false, int WPE = 1>
+__global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(WPE))) attnres_fwd_block_kernel(const FwdArgs<Rows> a) {
+  static_assert(G <= 64 || G == kBlock, "a wide group is the whole workgroup");
+  constexpr int kGroups = kBlock / G;
+  constexpr int NB = T * NBT;
+  __shared__ float xred[xred_floats<G>(2)];
+  const int lane = threadIdx.x % G;
+  const int group = group_index<G>();
+  const int D = a.width;
+  const int tail0 = D - a.rank;
+  const int S = a.n_sources;
+  const int64_t N = a.n_tokens;
+  const float inv_R = 1.0f / static_cast<float>(a.rank);
+  int phase = 0;
+
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * kGroups + group;
+  const int64_t tok0 = gid * T;
+  if (!QLDS && tok0 >= N) return;  // whole group idle
+  int64_t tok[T];
+  bool valid[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    valid[t] = tok0 + t < N;
+    tok[t] = valid[t] ? tok0 + t : N - 1;
+  }
+
+  __shared__ __attribute__((aligned(16))) uint32_t q_lds[QLDS ? G * CH * 4 : 1];
+  uint32_t qw[QLDS ? 1 : CH][4];
+  if constexpr (QLDS) {
+    uint32_t qt[CH][4];
+    load_query_words<G, CH>(a.query, lane, D, tail0, qt);
+    if (group == 0) {
+#pragma unroll
+      for (int c = 0; c < CH; ++c)
+        *reinterpret_cast<u32x4*>(&q_lds[(c * G + lane) * 4]) = u32x4{qt[c][0], qt[c][1], qt[c][2], qt[c][3]};
+    }
+    __syncthreads();
+  } else {
+    load_query_words<G, CH>(a.query, lane, D, tail0, qw);
+  }
+  uint32_t km[CH][4];
+  if constexpr (!NOMASK) key_masks<G, CH>(lane, D, tail0, km);
+  if (QLDS && tok0 >= N) return;  // whole group idle (after the workgroup's barrier)
+
+  const uint16_t* idle = a.src.row(0, tok[0]);
+  u32x4 ring[NB][CH];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const int s = j / T;
+    const ItemCursor at{tok[j % T], s < S ? s : 0, 1};
+    refill<G, CH, VEC>(a.src, at, s < S, idle, lane, D, ring[j]);
+  }
+
+  float acc[T][CH][kVec];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) acc[t][c][e] = 0.0f;
+  float run_max[T], run_sum[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    run_max[t] = -INFINITY;
+    run_sum[t] = 0.0f;
+  }
+
+  auto step = [&](int j, int s, bool refill_slot) __attribute__((always_inline)) {
+    const int t = j % T;
+    const int64_t token = tok[t];
+    float red[2] = {0.0f, 0.0f};
+    {
+      float ss1 = 0.0f, qd1 = 0.0f;
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const uint32_t w[4] = {ring[j][c].x, ring[j][c].y, ring[j][c].z, ring[j][c].w};
+        uint32_t qv[4];
+        if constexpr (QLDS) {
+          const u32x4 q4 = *reinterpret_cast<const u32x4*>(&q_lds[(c * G + lane) * 4]);
+          qv[0] = q4.x; qv[1] = q4.y; qv[2] = q4.z; qv[3] = q4.w;
+        } else {
+          qv[0] = qw[c][0]; qv[1] = qw[c][1]; qv[2] = qw[c][2]; qv[3] = qw[c][3];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t kw = NOMASK ? w[k] : (w[k] & km[c][k]);
+          if (k & 1) {
+            ss1 = dot2(kw, kw, ss1);
+            qd1 = dot2(kw, qv[k], qd1);
+          } else {
+            red[0] = dot2(kw, kw, red[0]);
+            red[1] = dot2(kw, qv[k], red[1]);
+          }
+        }
+      }
+      red[0] += ss1;
+      red[1] += qd1;
+    }
+    group_sum<G, 2>(red, xred, phase);
+    const float inv_rms = rsqrtf(fmaf(red[0], inv_R, a.eps));
+    const float z = red[1] * inv_rms * a.scale;
+    if (z > run_max[t]) {
+      const float alpha = __expf(run_max[t] - z);
+      run_sum[t] *= alpha;
+      run_max[t] = z;
+#pragma unroll
+      for (int c = 0; c < CH; ++c)
+#pragma unroll
+        for (int e = 0; e < kVec; ++e) acc[t][c][e] *= alpha;
+    }
+    {
+      const float w = __expf(z - run_max[t]);
+      run_sum[t] += w;
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const uint32_t wd[4] = {ring[j][c].x, ring[j][c].y, ring[j][c].z, ring[j][c].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          acc[t][c][2 * k] = fmaf(w, bf16_lo(wd[k]), acc[t][c][2 * k]);
+          acc[t][c][2 * k + 1] = fmaf(w, bf16_hi(wd[k]), acc[t][c][2 * k + 1]);
+        }
+      }
+    }
+    if (lane == 0 && valid[t]) {
+      a.logit[token * S + s] = z;
+      a.inv_rms[token * S + s] = inv_rms;
+    }
+    if (refill_slot) {
+      __builtin_amdgcn_sched_barrier(0);
+      const int sn = s + NBT;
+      const ItemCursor at{token, sn < S ? sn : 0, 1};
+      refill<G, CH, VEC>(a.src, at, sn < S, idle, lane, D, ring[j]);
+    }
+    if (s == S - 1) {
+      const float inv_sum = 1.0f / run_sum[t];
+#pragma unroll
+      for (int c = 0; c < CH; ++c)
+#pragma unroll
+        for (int e = 0; e < kVec; ++e) acc[t][c][e] *= inv_sum;
+      if (valid[t]) {
+        if (a.out_refine) {
+          store_row_refined<G, CH, NOMASK, VEC, true>(a.out + token * D, a.out_refine + token * D, lane, D, acc[t]);
+        } else {
+          store_row_refined<G, CH, NOMASK, VEC, false>(a.out + token * D, nullptr, lane, D, acc[t]);
+        }
+        if (lane == 0) {
+          a.stats[token] = run_max[t];
+          a.stats[N + token] = inv_sum;
+        }
+      }
+    }
+  };
+
+  const int full = S / NBT;
+  const int rem = S - full * NBT;
+  for (int r = 0; r < full; ++r) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) step(j, r * NBT + j / T, true);
+  }
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    if (j / T < rem) step(j, full * NBT + j / T, false);
+  }
+}
+
 // ----------------------------------------------------------------- backward
 
 // What the backward needs per token besides the value rows: dO (packed BF16),
@@ -1440,9 +1619,31 @@ int64_t resident_blocks() {
 // (4096), 262 -> 249 (8192); S = 13 at D = 2048: equal; S = 17: 216 -> 224.
 constexpr int kPersistentFwdMaxSources = 12;
 
+template <int G, int CH, int T, int NBT, bool NOMASK, bool VEC, class Rows>
+void launch_fwd_block(const FwdArgs<Rows>& a, hipStream_t stream) {
+  constexpr int64_t kTok = (kBlock / G) * T;
+  const int64_t blocks = (a.n_tokens + kTok - 1) / kTok;
+  hipLaunchKernelGGL((attnres_fwd_block_kernel<G, CH, T, NBT, NOMASK, VEC, Rows>), dim3(static_cast<unsigned>(blocks)),
+                     dim3(kBlock), 0, stream, a);
+}
+
+// Token blocks for few sources at D = R = 2048 (aligned, unmasked): two tokens
+// per wavefront, two rows of each in flight, one block per group.  Measured on
+// MI355X (forward alone, us, persistent one-token ring -> token blocks):
+// S = 9, N = 32768: 252.7 -> 234.6; S = 12, N = 16384: 161.8 -> 152.7; S = 5,
+// N = 32768: 157.9 -> 153.4.  Four tokens of one row each were slower at these
+// S (254.6, 159.8, 176.0), and at D = 1024 (32-lane groups) the same change
+// was mixed (S = 9: 123.8 -> 118.7; S = 12, R = 256: 78.4 -> 80.1).
+constexpr int kFwdBlockMinSources = 5;
+
 template <int G, int CH, bool NOMASK, bool VEC, class Rows>
 void launch_fwd(const FwdArgs<Rows>& a, hipStream_t stream) {
   constexpr int64_t kGroups = kBlock / G;
+  if constexpr (G == 64 && CH == 4 && NOMASK && VEC) {
+    if (a.n_sources >= kFwdBlockMinSources && a.n_sources <= kPersistentFwdMaxSources) {
+      return launch_fwd_block<G, CH, 2, 2, NOMASK, VEC>(a, stream);
+    }
+  }
   int64_t blocks = (a.n_tokens + kGroups - 1) / kGroups;
   if (a.n_sources <= kPersistentFwdMaxSources) {
     blocks = grid_blocks(a.n_tokens, G, resident_blocks<&attnres_fwd_kernel<G, CH, fwd_ring<CH>(), NOMASK, VEC, Rows>>());

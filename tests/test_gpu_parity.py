@@ -97,6 +97,35 @@ def test_aligned_fast_path_matches_oracle(width, rank, layout):
 
 
 @pytest.mark.parametrize("layout", ["packed", "list"])
+@pytest.mark.parametrize("sources,tokens", [(5, 1), (6, 3), (7, 4097), (9, 1031), (12, 2049)],
+                         ids=lambda v: str(v))
+def test_token_block_forward_matches_oracle(sources, tokens, layout):
+    """Aligned, unmasked rows of 2048 elements (R = D) of 5 to 12 sources take
+    the token-block forward, two tokens per group: a single token, odd token
+    counts (the last block repeats a token and stores nothing for it), reads
+    with and without the saved refinement; outputs, gradients and the saved
+    statistics against the oracle."""
+    torch.manual_seed(SEEDS[2] + sources * tokens)
+    width = rank = 2048
+    values = torch.randn(sources, tokens, width, device="cuda", dtype=torch.bfloat16)
+    values = (values * torch.linspace(0.5, 4, sources, device="cuda", dtype=torch.bfloat16)[:, None, None])
+    values.requires_grad_()
+    query = (torch.randn(rank, device="cuda", dtype=torch.bfloat16) / math.sqrt(rank)).requires_grad_()
+    upstream = torch.randn(tokens, width, device="cuda", dtype=torch.bfloat16)
+
+    def make(leaves, q):
+        return (tuple(leaves[0].unbind(0)) if layout == "list" else leaves[0]), q
+
+    print(f"token-block forward S={sources} N={tokens} layout={layout}", flush=True)
+    set_case(f"token-block forward S={sources} N={tokens} {layout}")
+    actual = attnres(make([values], query)[0], query)
+    grads = torch.autograd.grad(actual, (values, query), upstream)
+    expected, exact = both_oracles(make, [values], query, upstream)
+    compare_read((actual, *grads), expected, exact, ["out", "dv", "dq"], sources=sources)
+    check_statistics(make([values.detach()], query)[0], query.detach())
+
+
+@pytest.mark.parametrize("layout", ["packed", "list"])
 @pytest.mark.parametrize("sources,tokens", [(13, 1), (13, 3), (14, 4097), (16, 1030), (25, 2049), (49, 130), (129, 37)],
                          ids=lambda v: str(v))
 def test_token_block_backward_matches_oracle(sources, tokens, layout):
