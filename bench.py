@@ -12,7 +12,10 @@ N(0,1)/sqrt(R), dO N(0,1).
 
 Printed: ONE JSON line (rank 0).  ``value`` is the achieved algorithmic HBM
 bandwidth of the whole read in TB/s (bytes below / measured time per read);
-``ms_per_step`` is the time per read.  Algorithmic bytes per read:
+``ms_per_step`` is the time per read, from events around the K timed steps
+only; the forward / backward split (and the roofline's backward time) comes
+from a second pass of K steps with events around each forward and backward
+(``instrumented_pass``).  Algorithmic bytes per read:
 
     forward  = S*N*D*2 (values read) + N*D*2 (output write)
     backward = S*N*D*2 (values read) + N*D*2 (dO read) + S*N*D*2 (dvalues write)
@@ -856,19 +859,44 @@ def main(argv=None) -> int:
             events[2].record()
         return out, grads
 
+    # The graph-replay measurement runs first: about 0.4 s of the same read.  The
+    # GPU's clocks settle during the first ~15 ms of sustained load after an idle
+    # period (here the library's first call): a per-step trace of a cold start
+    # has steps 3-13 5-12% slower (backward 620-680 against 590 us, forward
+    # 296-311 against 277 us at c2), so with few warmup steps the eager
+    # steps below would time that transient instead of the read.
+    graph = graph_replay(values, query, grad_out, cfg)
     for _ in range(args.warmup):
+        step()
+    # The switch from graph replays to eager steps brings the same transient: in
+    # a per-step trace the eager steps 4-14 ran 5-12% slower whatever the
+    # warmup count before them.  K more untimed steps (reported below as
+    # settle_steps) let it pass, so the timed region measures the read.
+    for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
 
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    # The timed region: K steps between two events, nothing else on the stream.
+    # Per-step timing events cost the GPU about 4 us each (c2: 874 against 862 us
+    # per step), so the forward / backward split comes from a second, instrumented
+    # pass of K steps afterwards.
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record()
     for i in range(args.steps):
-        step(events[i])
+        step()
     stop.record()
     torch.cuda.synchronize()
     total_ms = start.elapsed_time(stop)
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    inst_start, inst_stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    inst_start.record()
+    for i in range(args.steps):
+        step(events[i])
+    inst_stop.record()
+    torch.cuda.synchronize()
+    instrumented_ms = inst_start.elapsed_time(inst_stop) / args.steps
     fwd_ms = [e[0].elapsed_time(e[1]) for e in events]
     bwd_ms = [e[1].elapsed_time(e[2]) for e in events]
 
@@ -901,6 +929,14 @@ def main(argv=None) -> int:
         "config": {"workload": cfg["name"], "sources": sources, "tokens": tokens,
                    "width": width, "rank": cfg["rank"], "layout": "packed",
                    "bytes_per_read": fwd_bytes + bwd_bytes},
+        "untimed_before_timed_region": {
+            "graph_replay": "11 rounds x 20 replays of the forward, backward and read graphs (graph_replay below)",
+            "warmup_steps": args.warmup, "settle_steps": args.steps,
+            "why": "the GPU's clocks settle during the first ~15 ms of sustained load after an idle period or a change "
+                   "of load; the timed region measures the read after that transient"},
+        "instrumented_pass": {"us_per_step": round(instrumented_ms * 1e3, 2),
+                              "what": "the same K steps with HIP events around each step's forward and backward "
+                                      "(the forward / backward split below); the events add their own GPU time"},
         "forward": {"us": round(fwd_avg * 1e3, 2), "bytes": fwd_bytes, "TB/s": round(fwd_tbs, 4),
                     "pct_of_peak": round(100 * fwd_tbs / HBM_PEAK_TBS, 2)},
         "backward": {"us": round(bwd_avg * 1e3, 2), "bytes": bwd_bytes, "TB/s": round(bwd_tbs, 4),
@@ -913,8 +949,8 @@ def main(argv=None) -> int:
                      "traffic": measured_traffic(args.config, "backward_bytes")},
         "cpu_baseline": None,
     }
-    # the same read through the C ABI, captured into a HIP graph and replayed
-    record["graph_replay"] = graph_replay(values, query, grad_out, cfg)
+    # the same read through the C ABI, captured into a HIP graph and replayed (measured first, above)
+    record["graph_replay"] = graph
     if not args.no_cpu_baseline:
         record["cpu_baseline"] = cpu_baseline(values.detach(), query.detach(), grad_out,
                                               args.cpu_budget, chunk=2048)
