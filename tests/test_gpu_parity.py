@@ -125,6 +125,32 @@ def test_token_block_forward_matches_oracle(sources, tokens, layout):
     check_statistics(make([values.detach()], query)[0], query.detach())
 
 
+@pytest.mark.parametrize("sources", [9, 13], ids=["forward_blocks", "backward_blocks"])
+def test_token_blocks_with_padded_strides(sources):
+    """The token-block kernels on packed values viewed out of a wider buffer:
+    rows 2112 elements apart (still 16-byte aligned) and sources a further
+    64 rows apart, so neither stride is N*D."""
+    torch.manual_seed(SEEDS[0] + sources)
+    tokens, width = 1027, 2048
+    big = torch.randn(sources, tokens + 64, width + 64, device="cuda", dtype=torch.bfloat16)
+    values = big[:, :tokens, :width]
+    values.mul_(torch.linspace(0.5, 4, sources, device="cuda", dtype=torch.bfloat16)[:, None, None])
+    values.requires_grad_()
+    assert values.stride() == ((tokens + 64) * (width + 64), width + 64, 1)
+    query = (torch.randn(width, device="cuda", dtype=torch.bfloat16) / math.sqrt(width)).requires_grad_()
+    upstream = torch.randn(tokens, width, device="cuda", dtype=torch.bfloat16)
+
+    def make(leaves, q):
+        return leaves[0], q
+
+    print(f"token blocks, padded strides S={sources}", flush=True)
+    set_case(f"token blocks padded strides S={sources}")
+    actual = attnres(values, query)
+    grads = torch.autograd.grad(actual, (values, query), upstream)
+    expected, exact = both_oracles(make, [values], query, upstream)
+    compare_read((actual, *grads), expected, exact, ["out", "dv", "dq"], sources=sources)
+
+
 @pytest.mark.parametrize("layout", ["packed", "list"])
 @pytest.mark.parametrize("sources,tokens", [(13, 1), (13, 3), (14, 4097), (16, 1030), (25, 2049), (49, 130), (129, 37)],
                          ids=lambda v: str(v))
