@@ -546,9 +546,10 @@ __global__ void __launch_bounds__(kBlock) attnres_fwd_kernel(const FwdArgs<Rows>
 // span) rather than several sources of one token, rows a power-of-two source
 // stride apart that can fall into the same DRAM banks.  Per-token arithmetic
 // is the one-token kernel's (same sums in the same order): bit-identical
-// results.  Used with T = 2, NBT = 2 (four rows in flight, two per token,
-// 206 VGPRs, two waves per SIMD) for 5 <= S <= 12 at D = R = 2048; see
-// launch_fwd for the measurements.  QLDS (query words from LDS) and WPE
+// results.  Used at D = R = 2048 with T = 2, NBT = 2 (four rows in flight,
+// two per token, 206 VGPRs, two waves per SIMD) for 5 <= S <= 12, and with
+// T = 4, NBT = 1 (one row per token, 259 registers, one wave per SIMD) for
+// S >= 24; see launch_fwd for the measurements.  QLDS (query words from LDS) and WPE
 // (waves per SIMD the compiler must fit) were measured variants and are not
 // used (T = 4 at two waves per SIMD: 317-349 against 299-323 us at c2).
 // Like the token-block backward, its timing is sensitive to code generation:
@@ -1636,6 +1637,16 @@ void launch_fwd_block(const FwdArgs<Rows>& a, hipStream_t stream) {
 // was mixed (S = 9: 123.8 -> 118.7; S = 12, R = 256: 78.4 -> 80.1).
 constexpr int kFwdBlockMinSources = 5;
 
+// Many sources at D = R = 2048: four tokens per wavefront, one row of each in
+// flight (one wave per SIMD).  Measured on MI355X (forward alone, us, one token
+// per group -> four), after a forward / after a backward of other values:
+// S = 25, N = 16384: 319.6 -> 318.4 / 320.6 -> 299.8; S = 49, N = 8192:
+// 298.4 -> 260.4 / 298.0 -> 261.5; but S = 16: 202.0 -> 199.3 / 202.8 -> 205.4.
+// Right after the backward of the same values (a benchmark loop repeating one
+// read) the one-token forward reads part of them from the memory-side cache and
+// is as fast or faster (S = 25: 286.6 against 288.8).
+constexpr int kFwdBlock4MinSources = 24;
+
 template <int G, int CH, bool NOMASK, bool VEC, class Rows>
 void launch_fwd(const FwdArgs<Rows>& a, hipStream_t stream) {
   constexpr int64_t kGroups = kBlock / G;
@@ -1643,6 +1654,7 @@ void launch_fwd(const FwdArgs<Rows>& a, hipStream_t stream) {
     if (a.n_sources >= kFwdBlockMinSources && a.n_sources <= kPersistentFwdMaxSources) {
       return launch_fwd_block<G, CH, 2, 2, NOMASK, VEC>(a, stream);
     }
+    if (a.n_sources >= kFwdBlock4MinSources) return launch_fwd_block<G, CH, 4, 1, NOMASK, VEC>(a, stream);
   }
   int64_t blocks = (a.n_tokens + kGroups - 1) / kGroups;
   if (a.n_sources <= kPersistentFwdMaxSources) {

@@ -125,7 +125,7 @@ def test_token_block_forward_matches_oracle(sources, tokens, layout):
     check_statistics(make([values.detach()], query)[0], query.detach())
 
 
-@pytest.mark.parametrize("sources", [9, 13], ids=["forward_blocks", "backward_blocks"])
+@pytest.mark.parametrize("sources", [9, 13, 25], ids=["forward_blocks_2", "backward_blocks", "both_blocks_4"])
 def test_token_blocks_with_padded_strides(sources):
     """The token-block kernels on packed values viewed out of a wider buffer:
     rows 2112 elements apart (still 16-byte aligned) and sources a further
