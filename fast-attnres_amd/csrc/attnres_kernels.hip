@@ -549,13 +549,13 @@ __global__ void __launch_bounds__(kBlock) attnres_fwd_kernel(const FwdArgs<Rows>
 // results.  Used at D = R = 2048 with T = 2, NBT = 2 (four rows in flight,
 // two per token, 206 VGPRs, two waves per SIMD) for 5 <= S <= 12, and with
 // T = 4, NBT = 1 (one row per token, 259 registers, one wave per SIMD) for
-// S >= 24; see launch_fwd for the measurements.  QLDS (query words from LDS) and WPE
-// (waves per SIMD the compiler must fit) were measured variants and are not
-// used (T = 4 at two waves per SIMD: 317-349 against 299-323 us at c2).
+// S >= 24; see launch_fwd for the measurements.  T = 4 forced to two waves
+// per SIMD (256 VGPRs) took 317-349 against 299-323 us at c2; the query words
+// read from LDS instead of registers made no difference.
 // Like the token-block backward, its timing is sensitive to code generation:
 // changes are measured before they are kept.
-template <int G, int CH, int T, int NBT, bool NOMASK, bool VEC, class Rows, bool QLDS = false, int WPE = 1>
-__global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(WPE))) attnres_fwd_block_kernel(const FwdArgs<Rows> a) {
+template <int G, int CH, int T, int NBT, bool NOMASK, bool VEC, class Rows>
+__global__ void __launch_bounds__(kBlock) attnres_fwd_block_kernel(const FwdArgs<Rows> a) {
   static_assert(G <= 64 || G == kBlock, "a wide group is the whole workgroup");
   constexpr int kGroups = kBlock / G;
   constexpr int NB = T * NBT;
@@ -571,7 +571,7 @@ __global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(WPE
 
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * kGroups + group;
   const int64_t tok0 = gid * T;
-  if (!QLDS && tok0 >= N) return;  // whole group idle
+  if (tok0 >= N) return;  // whole group idle
   int64_t tok[T];
   bool valid[T];
 #pragma unroll
@@ -580,23 +580,10 @@ __global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(WPE
     tok[t] = valid[t] ? tok0 + t : N - 1;
   }
 
-  __shared__ __attribute__((aligned(16))) uint32_t q_lds[QLDS ? G * CH * 4 : 1];
-  uint32_t qw[QLDS ? 1 : CH][4];
-  if constexpr (QLDS) {
-    uint32_t qt[CH][4];
-    load_query_words<G, CH>(a.query, lane, D, tail0, qt);
-    if (group == 0) {
-#pragma unroll
-      for (int c = 0; c < CH; ++c)
-        *reinterpret_cast<u32x4*>(&q_lds[(c * G + lane) * 4]) = u32x4{qt[c][0], qt[c][1], qt[c][2], qt[c][3]};
-    }
-    __syncthreads();
-  } else {
-    load_query_words<G, CH>(a.query, lane, D, tail0, qw);
-  }
+  uint32_t qw[CH][4];
+  load_query_words<G, CH>(a.query, lane, D, tail0, qw);
   uint32_t km[CH][4];
   if constexpr (!NOMASK) key_masks<G, CH>(lane, D, tail0, km);
-  if (QLDS && tok0 >= N) return;  // whole group idle (after the workgroup's barrier)
 
   const uint16_t* idle = a.src.row(0, tok[0]);
   u32x4 ring[NB][CH];
@@ -630,13 +617,7 @@ __global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(WPE
 #pragma unroll
       for (int c = 0; c < CH; ++c) {
         const uint32_t w[4] = {ring[j][c].x, ring[j][c].y, ring[j][c].z, ring[j][c].w};
-        uint32_t qv[4];
-        if constexpr (QLDS) {
-          const u32x4 q4 = *reinterpret_cast<const u32x4*>(&q_lds[(c * G + lane) * 4]);
-          qv[0] = q4.x; qv[1] = q4.y; qv[2] = q4.z; qv[3] = q4.w;
-        } else {
-          qv[0] = qw[c][0]; qv[1] = qw[c][1]; qv[2] = qw[c][2]; qv[3] = qw[c][3];
-        }
+        const uint32_t qv[4] = {qw[c][0], qw[c][1], qw[c][2], qw[c][3]};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           const uint32_t kw = NOMASK ? w[k] : (w[k] & km[c][k]);
@@ -1127,12 +1108,12 @@ __global__ void __launch_bounds__(kBlock) attnres_bwd_kernel(const BwdArgs<Rows,
 // item; slots wrap into the next block without draining.  With T = 4 the
 // kernel needs more than 256 registers (AGPRs hold the rest) and runs one
 // wave per SIMD: four rows in flight per wave.  T = 2 and 3 were slower
-// (680 and 700 us at c2).  It is launched with NOMASK only (the masked
-// instances spill).  Its timing is sensitive to code generation: a version
+// (680 and 700 us at c2).  It takes unmasked rows only (R = D = 2048): masked
+// instances spilled (224 bytes per lane).  Its timing is sensitive to code generation: a version
 // with a few equivalent source edits (a named request step, a hoisted idle
 // row) compiled to a kernel that took 670 us instead of 590 us at c2, so
 // changes here are measured before they are kept.
-template <int G, int CH, int T, bool NOMASK, bool VEC, class Rows, class Grads>
+template <int G, int CH, int T, bool VEC, class Rows, class Grads>
 __global__ void __launch_bounds__(kBlock) attnres_bwd_block_kernel(const BwdArgs<Rows, Grads> a) {
   static_assert(G == 64, "one wavefront per token");
   static_assert(std::is_same_v<Grads, PackedGrads> || std::is_same_v<Grads, ListGrads>, "BF16 dv rows");
@@ -1152,8 +1133,6 @@ __global__ void __launch_bounds__(kBlock) attnres_bwd_block_kernel(const BwdArgs
   int phase = 0;
 
   fill_query_lds<G, CH>(a.query, q_lds, tail0, D, R);
-  uint32_t km[CH][4];
-  if constexpr (!NOMASK) key_masks<G, CH>(lane, D, tail0, km);
   float dq[CH][kVec];
 #pragma unroll
   for (int c = 0; c < CH; ++c)
@@ -1184,7 +1163,6 @@ __global__ void __launch_bounds__(kBlock) attnres_bwd_block_kernel(const BwdArgs
       float red[T];
 #pragma unroll
       for (int t = 0; t < T; ++t) {
-        if constexpr (!NOMASK) mask_range<G, CH>(lane, D, pend[t].g);
         red[t] = token_delta<CH>(pend[t]);
       }
       group_sum<G, T>(red, xred, phase);
@@ -1267,8 +1245,7 @@ __global__ void __launch_bounds__(kBlock) attnres_bwd_block_kernel(const BwdArgs
           uint32_t out[4];
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
-            const uint32_t kw = NOMASK ? w[k] : (w[k] & km[c][k]);
-            const float k0 = bf16_lo(kw), k1 = bf16_hi(kw);
+            const float k0 = bf16_lo(w[k]), k1 = bf16_hi(w[k]);
             const float g0 = __uint_as_float(gw[k] << lo_shift), g1 = __uint_as_float(gw[k] & hi_mask);
             const float v0 = fmaf(cb, k0, fmaf(ca, qf[2 * k], p * g0));
             const float v1 = fmaf(cb, k1, fmaf(ca, qf[2 * k + 1], p * g1));
@@ -1276,7 +1253,7 @@ __global__ void __launch_bounds__(kBlock) attnres_bwd_block_kernel(const BwdArgs
             dq[c][2 * k + 1] = fmaf(ca, k1, dq[c][2 * k + 1]);
             out[k] = pack_bf16x2(v0, v1);
           }
-          if (valid && (NOMASK || d0 < D)) store_chunk<G, VEC>(grad_row, d0, D, u32x4{out[0], out[1], out[2], out[3]});
+          if (valid) store_chunk<G, VEC>(grad_row, d0, D, u32x4{out[0], out[1], out[2], out[3]});
         }
         __builtin_amdgcn_sched_barrier(0);  // refill the slot after its last use
         refill(t, wrap ? 0 : s + 1, nb, live_next);
@@ -1712,9 +1689,9 @@ constexpr int kBwdBlockMinSources = 13;
 
 template <int G, int CH, int T, bool VEC, class Rows, class Grads>
 int64_t launch_bwd_block(const BwdArgs<Rows, Grads>& a, hipStream_t stream) {
-  const int64_t resident = resident_blocks<&attnres_bwd_block_kernel<G, CH, T, true, VEC, Rows, Grads>>();
+  const int64_t resident = resident_blocks<&attnres_bwd_block_kernel<G, CH, T, VEC, Rows, Grads>>();
   const int64_t blocks = grid_blocks((a.n_tokens + T - 1) / T, G, kBwdGridPerResident * resident, a.max_grid);
-  hipLaunchKernelGGL((attnres_bwd_block_kernel<G, CH, T, true, VEC, Rows, Grads>), dim3(static_cast<unsigned>(blocks)),
+  hipLaunchKernelGGL((attnres_bwd_block_kernel<G, CH, T, VEC, Rows, Grads>), dim3(static_cast<unsigned>(blocks)),
                      dim3(kBlock), 0, stream, a);
   return blocks;
 }
