@@ -1552,7 +1552,9 @@ inline int64_t device_cus() {
 // S=25, N=16384, D=2048: 645 -> 637; S=9, N=8192, D=8192: 492 -> 483;
 // S=25, N=2048, D=1024: 54 -> 47 (R=D), 55 -> 48 (R=256); but at N=16384,
 // D=1024 two rows are 0.8% slower (occupancy 2 either way), and the
-// accumulating and element-wise variants spill with two.
+// accumulating and element-wise variants spill with two.  Rows of 8 chunks
+// (64 lanes, D <= 4096) keep two rows without spilling only unmasked, and
+// are 2-3% slower with them (S=25, N=16384, D=R=4096: 1273 -> 1316).
 template <int CH, bool VEC, bool ACC>
 constexpr bool kBwdTwoRowVariant = CH == 4 && VEC && !ACC;
 
