@@ -549,7 +549,8 @@ __global__ void __launch_bounds__(kBlock) attnres_fwd_kernel(const FwdArgs<Rows>
 // results.  Used at D = R = 2048 with T = 2, NBT = 2 (four rows in flight,
 // two per token, 206 VGPRs, two waves per SIMD) for 5 <= S <= 12, and with
 // T = 4, NBT = 1 (one row per token, 259 registers, one wave per SIMD) for
-// S >= 24; see launch_fwd for the measurements.  T = 4 forced to two waves
+// S >= 24, and for 64 lanes of 8 chunks (2048 < D <= 4096, masked or not) with
+// T = 2, NBT = 1 for S >= 13; see launch_fwd for the measurements.  T = 4 forced to two waves
 // per SIMD (256 VGPRs) took 317-349 against 299-323 us at c2; the query words
 // read from LDS instead of registers made no difference.
 // Like the token-block backward, its timing is sensitive to code generation:
@@ -1626,6 +1627,20 @@ constexpr int kFwdBlockMinSources = 5;
 // is as fast or faster (S = 25: 286.6 against 288.8).
 constexpr int kFwdBlock4MinSources = 24;
 
+// 64 lanes of 8 chunks (2048 < D <= 4096, 16-byte aligned rows), masked or
+// not, past the persistent range: two tokens per wavefront, one row of each
+// in flight.  Measured on MI355X (forward alone, N = 16384, us, one token per
+// group -> token blocks): D = 3072, R = D: S = 13: 336 -> 264, S = 25: 540 ->
+// 441, S = 48: 961 -> 797; D = 2560, R = 640: S = 25: 506 -> 404; D = R =
+// 4096: S = 13: 361 -> 331, S = 25: 601 -> 588, S = 48: 1061 -> 1064; D =
+// 4096, R = 1024: S = 13: 351 -> 327, S = 25: 601 -> 586, S = 48: 1059 ->
+// 1067.  Rows of fewer than 4096 elements leave some chunks of a one-token
+// group idle, and two tokens per wavefront keep more bytes in flight.  In the
+// persistent range (S <= 12) the one-token ring stays: S = 5: 135 -> 153
+// (D = 3072); two rows per token were slower everywhere.
+template <int G, int CH, bool VEC>
+constexpr bool kFwdBlock8Variant = G == 64 && CH == 8 && VEC;
+
 template <int G, int CH, bool NOMASK, bool VEC, class Rows>
 void launch_fwd(const FwdArgs<Rows>& a, hipStream_t stream) {
   constexpr int64_t kGroups = kBlock / G;
@@ -1634,6 +1649,9 @@ void launch_fwd(const FwdArgs<Rows>& a, hipStream_t stream) {
       return launch_fwd_block<G, CH, 2, 2, NOMASK, VEC>(a, stream);
     }
     if (a.n_sources >= kFwdBlock4MinSources) return launch_fwd_block<G, CH, 4, 1, NOMASK, VEC>(a, stream);
+  }
+  if constexpr (kFwdBlock8Variant<G, CH, VEC>) {
+    if (a.n_sources > kPersistentFwdMaxSources) return launch_fwd_block<G, CH, 2, 1, NOMASK, VEC>(a, stream);
   }
   int64_t blocks = (a.n_tokens + kGroups - 1) / kGroups;
   if (a.n_sources <= kPersistentFwdMaxSources) {

@@ -125,6 +125,37 @@ def test_token_block_forward_matches_oracle(sources, tokens, layout):
     check_statistics(make([values.detach()], query)[0], query.detach())
 
 
+@pytest.mark.parametrize("layout", ["packed", "list"])
+@pytest.mark.parametrize("sources,tokens,width,rank",
+                         [(13, 1, 4096, 4096), (13, 3, 3072, 3072), (16, 1027, 4096, 1024), (17, 2049, 2560, 640),
+                          (25, 130, 4000, 4000), (48, 517, 3072, 768)],
+                         ids=lambda v: str(v))
+def test_wide_token_block_forward_matches_oracle(sources, tokens, width, rank, layout):
+    """16-byte aligned rows of 2049 to 4096 elements (64 lanes of 8 chunks) of
+    more than 12 sources take the token-block forward, two tokens per group,
+    with and without key masks, full and partial rows (chunks past D idle): a
+    single token, odd token counts (the last block repeats a token and stores
+    nothing for it); outputs, gradients and the saved statistics against the
+    oracle."""
+    torch.manual_seed(SEEDS[2] + sources * tokens + width)
+    values = torch.randn(sources, tokens, width, device="cuda", dtype=torch.bfloat16)
+    values = (values * torch.linspace(0.5, 4, sources, device="cuda", dtype=torch.bfloat16)[:, None, None])
+    values.requires_grad_()
+    query = (torch.randn(rank, device="cuda", dtype=torch.bfloat16) / math.sqrt(rank)).requires_grad_()
+    upstream = torch.randn(tokens, width, device="cuda", dtype=torch.bfloat16)
+
+    def make(leaves, q):
+        return (tuple(leaves[0].unbind(0)) if layout == "list" else leaves[0]), q
+
+    print(f"wide token-block forward S={sources} N={tokens} D={width} R={rank} layout={layout}", flush=True)
+    set_case(f"wide token-block forward S={sources} N={tokens} D={width} R={rank} {layout}")
+    actual = attnres(make([values], query)[0], query)
+    grads = torch.autograd.grad(actual, (values, query), upstream)
+    expected, exact = both_oracles(make, [values], query, upstream)
+    compare_read((actual, *grads), expected, exact, ["out", "dv", "dq"], sources=sources)
+    check_statistics(make([values.detach()], query)[0], query.detach())
+
+
 @pytest.mark.parametrize("sources", [9, 13, 25], ids=["forward_blocks_2", "backward_blocks", "both_blocks_4"])
 def test_token_blocks_with_padded_strides(sources):
     """The token-block kernels on packed values viewed out of a wider buffer:
