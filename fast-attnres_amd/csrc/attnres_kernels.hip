@@ -1641,6 +1641,18 @@ constexpr int kFwdBlock4MinSources = 24;
 template <int G, int CH, bool VEC>
 constexpr bool kFwdBlock8Variant = G == 64 && CH == 8 && VEC;
 
+// 64 lanes of 4 chunks with rows shorter than 2048 (1024 < D < 2048, aligned,
+// so some chunks of a group idle), from kFwdBlockMinSources sources: the same
+// two tokens per wavefront, one row of each in flight.  Measured on MI355X
+// (forward alone, N = 16384, us, current -> token blocks): D = 1280, R = D:
+// S = 5: 61.9 -> 58.8, S = 13: 137.4 -> 109.2, S = 48: 388.3 -> 343.2;
+// D = 1536, R = D: S = 9: 100.7 -> 92.7, S = 13: 146.4 -> 124.7, S = 25:
+// 241.6 -> 229.9, S = 48: 425.1 -> 429.3; R = 384: S = 13: 140.4 -> 124.6.
+// Full rows of 2048 with key masks were mixed (R = 512: S = 13: 166.0 ->
+// 170.0, S = 48: 635.6 -> 570.0) and keep the one-token kernel.
+template <int G, int CH, bool NOMASK, bool VEC>
+constexpr bool kFwdBlockShortVariant = G == 64 && CH == 4 && !NOMASK && VEC;
+
 template <int G, int CH, bool NOMASK, bool VEC, class Rows>
 void launch_fwd(const FwdArgs<Rows>& a, hipStream_t stream) {
   constexpr int64_t kGroups = kBlock / G;
@@ -1652,6 +1664,11 @@ void launch_fwd(const FwdArgs<Rows>& a, hipStream_t stream) {
   }
   if constexpr (kFwdBlock8Variant<G, CH, VEC>) {
     if (a.n_sources > kPersistentFwdMaxSources) return launch_fwd_block<G, CH, 2, 1, NOMASK, VEC>(a, stream);
+  }
+  if constexpr (kFwdBlockShortVariant<G, CH, NOMASK, VEC>) {
+    if (a.n_sources >= kFwdBlockMinSources && a.width < G * CH * kVec) {
+      return launch_fwd_block<G, CH, 2, 1, NOMASK, VEC>(a, stream);
+    }
   }
   int64_t blocks = (a.n_tokens + kGroups - 1) / kGroups;
   if (a.n_sources <= kPersistentFwdMaxSources) {

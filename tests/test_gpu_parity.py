@@ -128,15 +128,18 @@ def test_token_block_forward_matches_oracle(sources, tokens, layout):
 @pytest.mark.parametrize("layout", ["packed", "list"])
 @pytest.mark.parametrize("sources,tokens,width,rank",
                          [(13, 1, 4096, 4096), (13, 3, 3072, 3072), (16, 1027, 4096, 1024), (17, 2049, 2560, 640),
-                          (25, 130, 4000, 4000), (48, 517, 3072, 768)],
+                          (25, 130, 4000, 4000), (48, 517, 3072, 768),
+                          (5, 1, 1536, 1536), (6, 3, 1280, 320), (9, 2051, 1536, 384), (48, 130, 1280, 1280)],
                          ids=lambda v: str(v))
-def test_wide_token_block_forward_matches_oracle(sources, tokens, width, rank, layout):
-    """16-byte aligned rows of 2049 to 4096 elements (64 lanes of 8 chunks) of
-    more than 12 sources take the token-block forward, two tokens per group,
-    with and without key masks, full and partial rows (chunks past D idle): a
-    single token, odd token counts (the last block repeats a token and stores
-    nothing for it); outputs, gradients and the saved statistics against the
-    oracle."""
+def test_two_token_block_forward_matches_oracle(sources, tokens, width, rank, layout):
+    """The token-block forward with two tokens per group and one row of each
+    in flight: 16-byte aligned rows of 2049 to 4096 elements (64 lanes of 8
+    chunks) of more than 12 sources, with and without key masks, full and
+    partial rows (chunks past D idle), and aligned rows of 1025 to 2047
+    elements (64 lanes of 4 chunks, some idle) of 5 sources and more,
+    including the few-source reads that save no refinement: a single token,
+    odd token counts (the last block repeats a token and stores nothing for
+    it); outputs, gradients and the saved statistics against the oracle."""
     torch.manual_seed(SEEDS[2] + sources * tokens + width)
     values = torch.randn(sources, tokens, width, device="cuda", dtype=torch.bfloat16)
     values = (values * torch.linspace(0.5, 4, sources, device="cuda", dtype=torch.bfloat16)[:, None, None])
@@ -147,8 +150,8 @@ def test_wide_token_block_forward_matches_oracle(sources, tokens, width, rank, l
     def make(leaves, q):
         return (tuple(leaves[0].unbind(0)) if layout == "list" else leaves[0]), q
 
-    print(f"wide token-block forward S={sources} N={tokens} D={width} R={rank} layout={layout}", flush=True)
-    set_case(f"wide token-block forward S={sources} N={tokens} D={width} R={rank} {layout}")
+    print(f"two-token block forward S={sources} N={tokens} D={width} R={rank} layout={layout}", flush=True)
+    set_case(f"two-token block forward S={sources} N={tokens} D={width} R={rank} {layout}")
     actual = attnres(make([values], query)[0], query)
     grads = torch.autograd.grad(actual, (values, query), upstream)
     expected, exact = both_oracles(make, [values], query, upstream)
