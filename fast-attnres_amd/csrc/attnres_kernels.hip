@@ -549,8 +549,10 @@ __global__ void __launch_bounds__(kBlock) attnres_fwd_kernel(const FwdArgs<Rows>
 // results.  Used at D = R = 2048 with T = 2, NBT = 2 (four rows in flight,
 // two per token, 206 VGPRs, two waves per SIMD) for 5 <= S <= 12, and with
 // T = 4, NBT = 1 (one row per token, 259 registers, one wave per SIMD) for
-// S >= 24, and for 64 lanes of 8 chunks (2048 < D <= 4096, masked or not) with
-// T = 2, NBT = 1 for S >= 13; see launch_fwd for the measurements.  T = 4 forced to two waves
+// S >= 24; with T = 2, NBT = 1 for 64 lanes of 8 chunks (2048 < D <= 4096,
+// masked or not) from S = 13, for shorter rows of 64 lanes of 4 chunks
+// (1024 < D < 2048) and for workgroup-wide groups (4096 < D <= 8192) from
+// S = 5; see launch_fwd for the measurements.  T = 4 forced to two waves
 // per SIMD (256 VGPRs) took 317-349 against 299-323 us at c2; the query words
 // read from LDS instead of registers made no difference.
 // Like the token-block backward, its timing is sensitive to code generation:
@@ -1653,6 +1655,17 @@ constexpr bool kFwdBlock8Variant = G == 64 && CH == 8 && VEC;
 template <int G, int CH, bool NOMASK, bool VEC>
 constexpr bool kFwdBlockShortVariant = G == 64 && CH == 4 && !NOMASK && VEC;
 
+// Workgroup-wide token groups (256 lanes of 4 chunks, 4096 < D <= 8192,
+// aligned), from kFwdBlockMinSources sources: two tokens per workgroup, one
+// row of each in flight.  Measured on MI355X (forward alone, N = 8192, us,
+// one token -> token blocks): D = 5120, R = D: S = 5: 120.1 -> 107.4, S = 25:
+// 487.7 -> 374.4, S = 48: 872.9 -> 700.9; D = 6144, R = 1536: S = 25: 493.1 ->
+// 452.8; D = 7168, R = D: S = 9: 228.6 -> 211.0; D = R = 8192: S = 9: 247.5 ->
+// 239.4, S = 48: 1160.8 -> 1134.0; R = 2048: S = 25: 615.3 -> 622.0.  Two
+// rows per token were slower than one.
+template <int G, int CH, bool VEC>
+constexpr bool kFwdBlockWideVariant = G == kBlock && CH == 4 && VEC;
+
 template <int G, int CH, bool NOMASK, bool VEC, class Rows>
 void launch_fwd(const FwdArgs<Rows>& a, hipStream_t stream) {
   constexpr int64_t kGroups = kBlock / G;
@@ -1664,6 +1677,9 @@ void launch_fwd(const FwdArgs<Rows>& a, hipStream_t stream) {
   }
   if constexpr (kFwdBlock8Variant<G, CH, VEC>) {
     if (a.n_sources > kPersistentFwdMaxSources) return launch_fwd_block<G, CH, 2, 1, NOMASK, VEC>(a, stream);
+  }
+  if constexpr (kFwdBlockWideVariant<G, CH, VEC>) {
+    if (a.n_sources >= kFwdBlockMinSources) return launch_fwd_block<G, CH, 2, 1, NOMASK, VEC>(a, stream);
   }
   if constexpr (kFwdBlockShortVariant<G, CH, NOMASK, VEC>) {
     if (a.n_sources >= kFwdBlockMinSources && a.width < G * CH * kVec) {
