@@ -130,16 +130,19 @@ def test_token_block_forward_matches_oracle(sources, tokens, layout):
                          [(13, 1, 4096, 4096), (13, 3, 3072, 3072), (16, 1027, 4096, 1024), (17, 2049, 2560, 640),
                           (25, 130, 4000, 4000), (48, 517, 3072, 768),
                           (5, 1, 1536, 1536), (6, 3, 1280, 320), (9, 2051, 1536, 384), (48, 130, 1280, 1280),
-                          (5, 1, 5120, 5120), (6, 3, 6144, 1536), (25, 131, 8192, 8192), (48, 17, 7168, 1792)],
+                          (5, 1, 5120, 5120), (6, 3, 6144, 1536), (25, 131, 8192, 8192), (48, 17, 7168, 1792),
+                          (5, 1, 512, 512), (6, 3, 384, 96), (25, 1027, 448, 448), (9, 2049, 768, 768),
+                          (13, 3, 520, 520), (48, 130, 640, 160)],
                          ids=lambda v: str(v))
 def test_two_token_block_forward_matches_oracle(sources, tokens, width, rank, layout):
-    """The token-block forward with two tokens per group and one row of each
-    in flight: 16-byte aligned rows of 2049 to 4096 elements (64 lanes of 8
-    chunks) of more than 12 sources, with and without key masks, full and
-    partial rows (chunks past D idle), and aligned rows of 1025 to 2047
-    elements (64 lanes of 4 chunks, some idle) and of 4097 to 8192 elements
-    (a workgroup of 256 lanes per token group) of 5 sources and more,
-    including the few-source reads that save no refinement: a single token,
+    """The token-block forward with two tokens per group: 16-byte aligned rows
+    of 2049 to 4096 elements (64 lanes of 8 chunks) of more than 12 sources,
+    with and without key masks, full and partial rows (chunks past D idle);
+    aligned rows of 1025 to 2047 elements (64 lanes of 4 chunks, some idle)
+    and of 4097 to 8192 elements (a workgroup of 256 lanes per token group) of
+    5 sources and more; 32-lane groups, two per wavefront, at 257 to 512
+    elements (two rows per token in flight) from 5 sources and at 513 to 1023
+    from 9; including the few-source reads that save no refinement: a single token,
     odd token counts (the last block repeats a token and stores nothing for
     it); outputs, gradients and the saved statistics against the oracle."""
     torch.manual_seed(SEEDS[2] + sources * tokens + width)
