@@ -552,7 +552,7 @@ __global__ void __launch_bounds__(kBlock) attnres_fwd_kernel(const FwdArgs<Rows>
 // S >= 24; with T = 2, NBT = 1 for 64 lanes of 8 chunks (2048 < D <= 4096,
 // masked or not) from S = 13, for shorter rows of 64 lanes of 4 chunks
 // (1024 < D < 2048) and for workgroup-wide groups (4096 < D <= 8192) from
-// S = 5; with 32-lane groups (two per wavefront) for 256 < D <= 512 (T = 2,
+// S = 5; with 32-lane groups (two per wavefront) for 128 < D <= 512 (T = 2,
 // NBT = 2) from S = 5 and for 512 < D < 1024 (T = 2, NBT = 1) from S = 9; see
 // launch_fwd for the measurements.  T = 4 forced to two waves
 // per SIMD (256 VGPRs) took 317-349 against 299-323 us at c2; the query words
@@ -1668,18 +1668,21 @@ constexpr bool kFwdBlockShortVariant = G == 64 && CH == 4 && !NOMASK && VEC;
 template <int G, int CH, bool VEC>
 constexpr bool kFwdBlockWideVariant = G == kBlock && CH == 4 && VEC;
 
-// 32-lane token groups (two per wavefront), aligned rows: at 2 chunks per lane
-// (256 < D <= 512) from kFwdBlockMinSources sources, two tokens per group with
-// two rows of each in flight; at 4 chunks (512 < D < 1024, some idle) from
+// 32-lane token groups (two per wavefront), aligned rows: at 1 or 2 chunks per
+// lane (128 < D <= 512) from kFwdBlockMinSources sources, two tokens per group
+// with two rows of each in flight; at 4 chunks (512 < D < 1024, some idle) from
 // kFwdBlockShort32MinSources, one row of each.  Measured on MI355X (forward
 // alone, N = 16384, us, one token -> token blocks): D = 512, R = D: S = 5:
 // 28.3 -> 23.3, S = 25: 85.2 -> 77.7, S = 48: 153.2 -> 146.3; D = 384: S = 9:
 // 38.0 -> 30.8, S = 25: 83.0 -> 64.6, S = 48: 140.3 -> 126.2; D = 768, R = D:
 // S = 9: 53.7 -> 53.0, S = 25: 125.1 -> 111.4, S = 48: 214.1 -> 200.6; D =
-// 640, R = 160: S = 25: 115.1 -> 101.5; but S = 5: 37.2 -> 38.9 (D = 768).
-// Full rows of 1024 were within +-3% either way and keep the one-token kernel.
+// 640, R = 160: S = 25: 115.1 -> 101.5; but S = 5: 37.2 -> 38.9 (D = 768);
+// D = 256 (1 chunk): S = 9: 24.8 -> 23.4, S = 25: 51.2 -> 45.8; D = 200: S =
+// 48: 86.6 -> 79.8.  Full rows of 1024 were within +-3% either way and keep
+// the one-token kernel, as do 16-lane groups (D <= 128: within +-1.5%) and
+// rows that are not 16-byte aligned (D = 3000, 1000, 5000: within +-1%).
 template <int G, int CH, bool VEC>
-constexpr bool kFwdBlock32x2Variant = G == 32 && CH == 2 && VEC;
+constexpr bool kFwdBlock32NarrowVariant = G == 32 && CH <= 2 && VEC;
 template <int G, int CH, bool NOMASK, bool VEC>
 constexpr bool kFwdBlock32x4Variant = G == 32 && CH == 4 && !NOMASK && VEC;
 constexpr int kFwdBlockShort32MinSources = 9;
@@ -1699,7 +1702,7 @@ void launch_fwd(const FwdArgs<Rows>& a, hipStream_t stream) {
   if constexpr (kFwdBlockWideVariant<G, CH, VEC>) {
     if (a.n_sources >= kFwdBlockMinSources) return launch_fwd_block<G, CH, 2, 1, NOMASK, VEC>(a, stream);
   }
-  if constexpr (kFwdBlock32x2Variant<G, CH, VEC>) {
+  if constexpr (kFwdBlock32NarrowVariant<G, CH, VEC>) {
     if (a.n_sources >= kFwdBlockMinSources) return launch_fwd_block<G, CH, 2, 2, NOMASK, VEC>(a, stream);
   }
   if constexpr (kFwdBlock32x4Variant<G, CH, NOMASK, VEC>) {

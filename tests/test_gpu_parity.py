@@ -132,7 +132,7 @@ def test_token_block_forward_matches_oracle(sources, tokens, layout):
                           (5, 1, 1536, 1536), (6, 3, 1280, 320), (9, 2051, 1536, 384), (48, 130, 1280, 1280),
                           (5, 1, 5120, 5120), (6, 3, 6144, 1536), (25, 131, 8192, 8192), (48, 17, 7168, 1792),
                           (5, 1, 512, 512), (6, 3, 384, 96), (25, 1027, 448, 448), (9, 2049, 768, 768),
-                          (13, 3, 520, 520), (48, 130, 640, 160)],
+                          (13, 3, 520, 520), (48, 130, 640, 160), (5, 3, 256, 256), (25, 1027, 200, 40)],
                          ids=lambda v: str(v))
 def test_two_token_block_forward_matches_oracle(sources, tokens, width, rank, layout):
     """The token-block forward with two tokens per group: 16-byte aligned rows
@@ -140,7 +140,7 @@ def test_two_token_block_forward_matches_oracle(sources, tokens, width, rank, la
     with and without key masks, full and partial rows (chunks past D idle);
     aligned rows of 1025 to 2047 elements (64 lanes of 4 chunks, some idle)
     and of 4097 to 8192 elements (a workgroup of 256 lanes per token group) of
-    5 sources and more; 32-lane groups, two per wavefront, at 257 to 512
+    5 sources and more; 32-lane groups, two per wavefront, at 129 to 512
     elements (two rows per token in flight) from 5 sources and at 513 to 1023
     from 9; including the few-source reads that save no refinement: a single token,
     odd token counts (the last block repeats a token and stores nothing for
