@@ -164,26 +164,29 @@ def test_two_token_block_forward_matches_oracle(sources, tokens, width, rank, la
     check_statistics(make([values.detach()], query)[0], query.detach())
 
 
-@pytest.mark.parametrize("sources", [9, 13, 25], ids=["forward_blocks_2", "backward_blocks", "both_blocks_4"])
-def test_token_blocks_with_padded_strides(sources):
+@pytest.mark.parametrize("sources,width,rank", [(9, 2048, 2048), (13, 2048, 2048), (25, 2048, 2048),
+                                                (13, 3072, 768), (5, 5120, 5120), (9, 384, 384), (9, 1536, 1536)],
+                         ids=["forward_blocks_2", "backward_blocks", "both_blocks_4", "forward_64x8",
+                              "forward_256", "forward_32x2", "forward_64x4_short"])
+def test_token_blocks_with_padded_strides(sources, width, rank):
     """The token-block kernels on packed values viewed out of a wider buffer:
-    rows 2112 elements apart (still 16-byte aligned) and sources a further
+    rows D + 64 elements apart (still 16-byte aligned) and sources a further
     64 rows apart, so neither stride is N*D."""
-    torch.manual_seed(SEEDS[0] + sources)
-    tokens, width = 1027, 2048
+    torch.manual_seed(SEEDS[0] + sources + width)
+    tokens = 1027
     big = torch.randn(sources, tokens + 64, width + 64, device="cuda", dtype=torch.bfloat16)
     values = big[:, :tokens, :width]
     values.mul_(torch.linspace(0.5, 4, sources, device="cuda", dtype=torch.bfloat16)[:, None, None])
     values.requires_grad_()
     assert values.stride() == ((tokens + 64) * (width + 64), width + 64, 1)
-    query = (torch.randn(width, device="cuda", dtype=torch.bfloat16) / math.sqrt(width)).requires_grad_()
+    query = (torch.randn(rank, device="cuda", dtype=torch.bfloat16) / math.sqrt(rank)).requires_grad_()
     upstream = torch.randn(tokens, width, device="cuda", dtype=torch.bfloat16)
 
     def make(leaves, q):
         return leaves[0], q
 
-    print(f"token blocks, padded strides S={sources}", flush=True)
-    set_case(f"token blocks padded strides S={sources}")
+    print(f"token blocks, padded strides S={sources} D={width} R={rank}", flush=True)
+    set_case(f"token blocks padded strides S={sources} D={width} R={rank}")
     actual = attnres(values, query)
     grads = torch.autograd.grad(actual, (values, query), upstream)
     expected, exact = both_oracles(make, [values], query, upstream)
