@@ -120,9 +120,16 @@ def _contiguous(tensor: Tensor) -> Tensor:
     return tensor if tensor.is_contiguous() else tensor.contiguous()
 
 
+# torch's raw current-stream query skips building a Python Stream object (a
+# few microseconds per launch); builds without it use the public Stream.
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(device: torch.device) -> int:
-    """The current stream's handle on ``device`` (no Python Stream object)."""
-    return torch._C._cuda_getCurrentRawStream(device.index)
+    """The current stream's handle on ``device``."""
+    if _RAW_STREAM is not None:
+        return _RAW_STREAM(device.index)
+    return torch.cuda.current_stream(device).cuda_stream
 
 
 _NO_SWITCH = contextlib.nullcontext()

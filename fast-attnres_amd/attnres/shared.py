@@ -68,9 +68,17 @@ class _GatherRead(ctypes.Structure):
 assert ctypes.sizeof(_GatherRead) == 6 * 8 and _GatherRead.position.offset == 4 * 8
 
 
+_GRAPH_TASK_ID = getattr(torch._C, "_current_graph_task_id", None)
+
+
 def _pass_id() -> int:
-    """The running backward pass: autograd's graph-task id (-1 outside one)."""
-    return torch._C._current_graph_task_id()
+    """The running backward pass: autograd's graph-task id (-1 outside one).
+    No public torch API tells one backward pass from the next; a torch build
+    without this query cannot run shared-source reads and says so."""
+    if _GRAPH_TASK_ID is None:
+        raise RuntimeError("SharedSources and SourceBank need torch._C._current_graph_task_id, "
+                           "which this torch build does not provide")
+    return _GRAPH_TASK_ID()
 
 
 class _SharedState:
