@@ -166,6 +166,12 @@ def measured_traffic(config: str, key: str) -> int | None:
     return int(json.loads(path.read_text()).get(key)) or None
 
 
+def _traffic_field(config: str, key: str):
+    """Another field of profiles/attnres_<config>_hbm_traffic.json (None when absent)."""
+    path = ROOT / "profiles" / f"attnres_{config}_hbm_traffic.json"
+    return json.loads(path.read_text()).get(key) if path.is_file() else None
+
+
 def copy_probe(gib: float = 1.0, reps: int = 5) -> None:
     """Streams of known size, for scaling the FETCH_SIZE / WRITE_SIZE counters:
     a device-to-device copy (torch), and the library's BF16 partial-sum kernel
@@ -302,7 +308,8 @@ def graph_replay(values, query, grad_out, cfg: dict, replays: int = 20, rounds: 
     dev = packed.device
     out = torch.empty(N, width, device=dev, dtype=torch.bfloat16)
     # the product path's save/recompute policy: no refinement for small reads
-    refine = torch.empty(N if lib.attnres_hip_saves_refinement(S) else 0, width, device=dev, dtype=torch.int8)
+    refine = torch.empty(N if lib.attnres_hip_saves_refinement_for(S, width, rank) else 0, width, device=dev,
+                         dtype=torch.int8)
     logit, inv_rms = torch.empty(N, S, device=dev), torch.empty(N, S, device=dev)
     stats = torch.empty(2, N, device=dev)
     dv = torch.empty_like(packed)
@@ -533,7 +540,51 @@ def _sweep_one_backward_pass(values, query, grad_out, max_sources: int, steps: i
     return start.elapsed_time(stop) / steps
 
 
-def run_sweep(cfg: dict, steps: int, warmup: int) -> dict:
+def sweep_cpu_baseline(cfg: dict, budget_s: float, samples=(1, 12, 24, 48)) -> dict:
+    """The CPU oracle's time for one c5 step: for each (D, R), a few reads
+    (S in ``samples``) are timed by ``cpu_baseline`` on token chunks of their
+    own inputs (``budget_s`` split evenly), a least-squares line in S is fitted
+    to their per-read times (the oracle's work is linear in S), and the line
+    is summed over S = 1..48.  Inputs are drawn on the CPU (no GPU memory)."""
+    tokens, max_sources = cfg["batch"][0], cfg["sources"]
+    drawn = min(tokens, 1024)  # tokens drawn per sampled read; the oracle's time per token is scaled up
+    per_sample = budget_s / (len(cfg["widths"]) * 2 * len(samples))
+    total_s, total_bytes, fits, record = 0.0, 0, [], None
+    for width in cfg["widths"]:
+        for rank in (width, width // 4):
+            times = []
+            for sources in samples:
+                values, query, grad_out = make_inputs(dict(sources=sources, batch=(drawn,), width=width, rank=rank,
+                                                           input_device="cpu"), "cpu", seed=width + rank)
+                record = cpu_baseline(values, query, grad_out, per_sample, chunk=256)
+                times.append(record["us_per_read"] * 1e-6 * tokens / drawn)
+            n = len(samples)
+            mean_s, mean_t = sum(samples) / n, sum(times) / n
+            slope = (sum((s - mean_s) * (t - mean_t) for s, t in zip(samples, times))
+                     / sum((s - mean_s) ** 2 for s in samples))
+            intercept = mean_t - slope * mean_s
+            step_s = sum(intercept + slope * s for s in range(1, max_sources + 1))
+            total_s += step_s
+            total_bytes += sum(sum(read_bytes(s, tokens, width)) for s in range(1, max_sources + 1))
+            fits.append({"width": width, "rank": rank, "samples_S_s": [[s, round(t, 4)] for s, t in zip(samples, times)],
+                         "s_per_step": round(step_s, 3)})
+    steps = len(fits)
+    return {
+        "value": round(total_bytes / total_s / 1e12, 6), "unit": "TB/s",
+        "ms_per_step": round(total_s / steps * 1e3, 1),
+        "cores": record["cores"], "host_cpus_visible": record["host_cpus_visible"], "cpu_model": record["cpu_model"],
+        "kind": "port",
+        "sample": (f"CPU FP32 eager oracle (oracle/oracle.py, {record['cores']} threads): for each (D, R), reads of "
+                   f"S = {', '.join(map(str, samples))} timed on token chunks of 256 of {drawn} tokens drawn as the "
+                   f"sweep draws its inputs, scaled to {tokens} tokens ({budget_s:.0f} s in all), per-read time "
+                   f"fitted linear in S and summed over S = 1..{max_sources}; "
+                   f"ms_per_step is the mean over the {steps} (D, R) steps, value their algorithmic bytes over the "
+                   f"summed time"),
+        "fits": fits,
+    }
+
+
+def run_sweep(cfg: dict, steps: int, warmup: int, cpu_budget: float | None = None) -> dict:
     """c5: one packed read per S = 1..48 (N=16384) for each D and R in
     {D, D/4}; the value rows of a read are the first S sources of one
     [48, N, D] tensor (a view, no copy)."""
@@ -601,8 +652,12 @@ def run_sweep(cfg: dict, steps: int, warmup: int) -> dict:
         # backward kernels take about half of the traced time): algorithmic bytes / time
         "roofline": {"bound": "hbm", "kernel": "every read of the sweep: forward + backward ops",
                      "achieved": round(value * 1e3, 1), "peak": HBM_PEAK_TBS * 1e3, "unit": "GB/s",
-                     "frac": round(value / HBM_PEAK_TBS, 4), "traffic": None},
-        "cpu_baseline": None,
+                     "frac": round(value / HBM_PEAK_TBS, 4),
+                     # measured HBM bytes of the sweep's kernels per step (mean over the four (D, R)
+                     # steps), from rocprofv3 counters (profiles/attnres_c5_hbm_traffic.json)
+                     "traffic": measured_traffic("c5", "bytes_per_step"),
+                     "traffic_ratio": _traffic_field("c5", "ratio")},
+        "cpu_baseline": None if cpu_budget is None else sweep_cpu_baseline(cfg, cpu_budget),
     }
 
 
@@ -868,7 +923,7 @@ def main(argv=None) -> int:
             result = run_model(cfg, args.steps, args.warmup, args.model_variant, args.autocast == "bf16")
         else:
             run = {"c4": run_block_schedule, "c5": run_sweep, "policy": run_policy}[args.config]
-            if args.config == "c4":
+            if args.config in ("c4", "c5"):
                 result = run(cfg, args.steps, args.warmup, None if args.no_cpu_baseline else args.cpu_budget)
             else:
                 result = run(cfg, args.steps, args.warmup)

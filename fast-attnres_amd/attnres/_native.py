@@ -33,6 +33,7 @@ SIGNATURES = {
     "attnres_hip_version": (ctypes.c_char_p, []),
     "attnres_hip_last_error": (ctypes.c_char_p, []),
     "attnres_hip_saves_refinement": (ctypes.c_int, [_i64]),
+    "attnres_hip_saves_refinement_for": (ctypes.c_int, [_i64, _i64, _i64]),
     "attnres_hip_dq_workspace_elems": (_i64, [_i64, _i64, _i64]),
     "attnres_hip_packed_forward": (ctypes.c_int, [
         _c_void_p, _i64, _i64, _i64, _i64, _i64, _c_void_p, _i64, _f32, _f32,

@@ -32,7 +32,10 @@ more than ``RECOMPUTE_MAX_SOURCES`` sources -- the BF16 output plus one
 refinement byte per element (together the FP32 mix to ulp/512, for
 ``delta = <dO, o>``).  Smaller reads save neither: ``out_refine`` is
 ``[0, D]`` and their backward derives delta from the value rows it reads
-anyway.  The reference makes the same structural choice
+anyway; so do reads of up to ``KEYRES_MAX_SOURCES`` sources whose key is the
+last 512 or 1024 elements of a 2048- or 4096-wide row (`keyres_key_chunks`:
+the key-resident backward holds the key coordinates of a token's rows until
+delta is complete).  The reference makes the same structural choice
 (`fla_full_sources._should_save_mixed`, `fla_full_sources.py:146-161`:
 recompute for S <= 3) but saves an FP32 copy of the output for larger reads
 (`fixed_tail.py:917-919`): four extra bytes per element written in the
@@ -56,19 +59,41 @@ from . import _native
 _F32 = torch.float32
 _BF16 = torch.bfloat16
 
-# Save/recompute policy (attnres_hip.h ATTNRES_RECOMPUTE_MAX_SOURCES).
+# Save/recompute policy (attnres_hip.h ATTNRES_RECOMPUTE_MAX_SOURCES,
+# ATTNRES_KEYRES_MAX_SOURCES; attnres_hip_saves_refinement_for).
 RECOMPUTE_MAX_SOURCES = 6
+KEYRES_MAX_SOURCES = 16
+_KEY_COLUMN = 512  # elements per chunk column of a 64-lane row (64 lanes x 8)
 
 
-def saves_refinement(sources: int) -> bool:
-    """Whether a read of ``sources`` sources saves its output refinement for
-    the backward (else the backward recomputes delta from the value rows;
-    reference `fla_full_sources._should_save_mixed`, `fla_full_sources.py:146-161`)."""
-    return sources > RECOMPUTE_MAX_SOURCES
+def keyres_key_chunks(width: int, rank: int) -> int:
+    """Chunk columns of the key when the key-resident backward applies to a
+    read of this width and rank: rows of 2048 or 4096 elements (64-lane
+    groups, every chunk in range) whose key is their last 512 or 1024
+    elements; 0 otherwise."""
+    if not 1024 < width <= 4096:
+        return 0
+    chunks = 4 if width <= 2048 else 8
+    if width != chunks * _KEY_COLUMN or rank >= width or rank % _KEY_COLUMN:
+        return 0
+    key_chunks = rank // _KEY_COLUMN
+    return key_chunks if key_chunks <= 2 else 0
 
 
-def _refine_rows(sources: int, tokens: int) -> int:
-    return tokens if saves_refinement(sources) else 0
+def saves_refinement(sources: int, width: int, rank: int) -> bool:
+    """Whether a read saves its output refinement for the backward (else the
+    backward takes delta from the value rows: every read of at most
+    ``RECOMPUTE_MAX_SOURCES`` sources, and reads of at most
+    ``KEYRES_MAX_SOURCES`` whose key the key-resident backward holds).
+    Reference `fla_full_sources._should_save_mixed`, `fla_full_sources.py:146-161`,
+    keys on the source count alone."""
+    if sources <= RECOMPUTE_MAX_SOURCES:
+        return False
+    return not (sources <= KEYRES_MAX_SOURCES and keyres_key_chunks(width, rank) > 0)
+
+
+def _refine_rows(sources: int, tokens: int, width: int, rank: int) -> int:
+    return tokens if saves_refinement(sources, width, rank) else 0
 
 
 def _pointer(tensor: Tensor) -> int | None:
@@ -193,14 +218,15 @@ def packed_forward_impl(values: Tensor, query: Tensor, eps: float, scale: float,
                          device_types="cuda", tags=_OP_TAGS)
 def packed_forward(values: Tensor, query: Tensor, eps: float,
                    scale: float) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
-    return packed_forward_impl(values, query, eps, scale, saves_refinement(int(values.shape[0])))
+    return packed_forward_impl(values, query, eps, scale,
+                               saves_refinement(int(values.shape[0]), int(values.shape[2]), query.numel()))
 
 
 @packed_forward.register_fake
 def _packed_forward_fake(values, query, eps, scale):
     sources, tokens, width = values.shape
     return (values.new_empty((tokens, width)),
-            values.new_empty((_refine_rows(sources, tokens), width), dtype=torch.int8),
+            values.new_empty((_refine_rows(sources, tokens, width, query.numel()), width), dtype=torch.int8),
             values.new_empty((tokens, sources), dtype=_F32),
             values.new_empty((tokens, sources), dtype=_F32),
             values.new_empty((2, tokens), dtype=_F32))
@@ -287,7 +313,8 @@ class _PackedRead(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, values: Tensor, query: Tensor, eps: float, scale: float):
-        outputs = packed_forward_impl(values, query, eps, scale, saves_refinement(int(values.shape[0])))
+        outputs = packed_forward_impl(values, query, eps, scale,
+                                      saves_refinement(int(values.shape[0]), int(values.shape[-1]), query.numel()))
         _packed_setup_context(ctx, (values, query, eps, scale), outputs)
         return outputs
 
@@ -358,7 +385,8 @@ def sources_forward_impl(sources: list[Tensor], query: Tensor, eps: float, scale
                          device_types="cuda", tags=_OP_TAGS)
 def sources_forward(sources: list[Tensor], query: Tensor, eps: float,
                     scale: float) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
-    return sources_forward_impl(sources, query, eps, scale, saves_refinement(len(sources)))
+    return sources_forward_impl(sources, query, eps, scale,
+                                saves_refinement(len(sources), int(sources[0].shape[-1]), query.numel()))
 
 
 @sources_forward.register_fake
@@ -366,7 +394,8 @@ def _sources_forward_fake(sources, query, eps, scale):
     first = sources[0]
     count, tokens = len(sources), _rows_of(first.shape)
     return (first.new_empty(first.shape),
-            first.new_empty((_refine_rows(count, tokens), int(first.shape[-1])), dtype=torch.int8),
+            first.new_empty((_refine_rows(count, tokens, int(first.shape[-1]), query.numel()), int(first.shape[-1])),
+                            dtype=torch.int8),
             first.new_empty((tokens, count), dtype=_F32),
             first.new_empty((tokens, count), dtype=_F32),
             first.new_empty((2, tokens), dtype=_F32))
@@ -449,7 +478,8 @@ class _SourcesRead(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, query: Tensor, eps: float, scale: float, *sources: Tensor):
-        outputs = sources_forward_impl(list(sources), query, eps, scale, saves_refinement(len(sources)))
+        outputs = sources_forward_impl(list(sources), query, eps, scale,
+                                       saves_refinement(len(sources), int(sources[0].shape[-1]), query.numel()))
         _sources_setup_context(ctx, (sources, query, eps, scale), outputs)
         return outputs
 
@@ -476,7 +506,7 @@ def sources_attnres(sources: tuple[Tensor, ...], query: Tensor, eps: float,
 
 
 __all__ = [
-    "RECOMPUTE_MAX_SOURCES", "packed_attnres", "packed_backward", "packed_backward_impl", "packed_forward",
+    "KEYRES_MAX_SOURCES", "RECOMPUTE_MAX_SOURCES", "keyres_key_chunks", "packed_attnres", "packed_backward", "packed_backward_impl", "packed_forward",
     "packed_forward_impl", "prepare_rows", "row_stride", "saves_refinement", "sources_attnres", "sources_backward",
     "sources_backward_impl", "sources_forward", "sources_forward_impl",
 ]

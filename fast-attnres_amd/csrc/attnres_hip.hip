@@ -328,10 +328,12 @@ bool set_accumulate(BwdArgs<Rows, Grads>& a, const uint8_t* flags, int64_t n_sou
 bool aligned16_or_null(const void* p) { return !p || aligned16(p); }
 
 // Backward without the saved output: the recompute kernel, for small reads only.
-int check_recompute(bool recompute, int64_t S, const char* name) {
-  if (recompute && S > kRecomputeMaxSources)
-    return fail(ATTNRES_ERR_SHAPE, "%s without out_refine needs n_sources <= %d (got %lld)", name,
-                kRecomputeMaxSources, (long long)S);
+int check_recompute(bool recompute, int64_t S, int64_t D, int64_t R, const char* name) {
+  if (recompute && !recomputes(S, D, R))
+    return fail(ATTNRES_ERR_SHAPE,
+                "%s without out_refine needs n_sources <= %d, or <= %d with a key of 512 or 1024 whole "
+                "columns of a 2048- or 4096-wide row (got n_sources=%lld, width=%lld, rank=%lld)",
+                name, kRecomputeMaxSources, kKeyResMaxSources, (long long)S, (long long)D, (long long)R);
   return ATTNRES_OK;
 }
 
@@ -352,6 +354,10 @@ const char* attnres_hip_version(void) { return "2.0.1+mi355x.1"; }
 const char* attnres_hip_last_error(void) { return g_error; }
 
 int attnres_hip_saves_refinement(int64_t n_sources) { return n_sources > kRecomputeMaxSources ? 1 : 0; }
+
+int attnres_hip_saves_refinement_for(int64_t n_sources, int64_t width, int64_t rank) {
+  return recomputes(n_sources, width, rank) ? 0 : 1;
+}
 
 int64_t attnres_hip_dq_workspace_elems(int64_t n_tokens, int64_t width, int64_t rank) {
   if (check_shape(1, n_tokens, width, rank) != ATTNRES_OK) return -1;
@@ -403,20 +409,22 @@ int packed_backward(const void* values, int64_t source_stride, int64_t row_strid
                     const void* out, const int8_t* out_refine, const void* grad_out, const float* logit,
                     const float* inv_rms, const float* stats, void* grad_values, void* grad_query,
                     float* dq_workspace, int64_t dq_workspace_elems, const uint8_t* accumulate, bool need_flags,
-                    void* stream, bool fit_grid = false) {
+                    void* stream, bool fit_grid = false, const char* entry = nullptr) {
   constexpr bool kF32 = kF32Grads<Grads>;
   constexpr bool kCoef = std::is_same_v<Grads, CoefSink>;
-  const char* name = kCoef ? "attnres_hip_packed_backward_coef"
-                     : kF32 ? "attnres_hip_packed_backward_accumulate_f32"
-                     : need_flags ? "attnres_hip_packed_backward_accumulate" : "attnres_hip_packed_backward";
+  const char* name = entry                ? entry
+                     : kCoef              ? "attnres_hip_packed_backward_coef"
+                     : kF32               ? "attnres_hip_packed_backward_accumulate_f32"
+                     : need_flags         ? "attnres_hip_packed_backward_accumulate"
+                                          : "attnres_hip_packed_backward";
   int st = check_shape(n_sources, n_tokens, width, rank);
   if (st) return st;
   const bool recompute = !kCoef && !need_flags && !out_refine;
   if (!values || !query || (!recompute && (!out || !out_refine)) || !grad_out || !logit || !inv_rms || !stats ||
       !grad_values || !grad_query || !dq_workspace || (need_flags && !accumulate))
     return fail(ATTNRES_ERR_NULL_POINTER, "null pointer argument to %s", name);
-  if ((st = check_recompute(recompute, n_sources, name))) return st;
-  if (source_stride < 0 || row_stride < 0) return fail(ATTNRES_ERR_STRIDE, "negative stride");
+  if ((st = check_recompute(recompute, n_sources, width, rank, name))) return st;
+  if (source_stride < 0 || row_stride < 0) return fail(ATTNRES_ERR_STRIDE, "negative stride in %s", name);
   if ((st = check_scalars(1.0f, scale, false))) return st;
   const int64_t need = workspace_elems(n_tokens, width, rank);
   if (dq_workspace_elems < (fit_grid ? 2 * rank : need))
@@ -503,15 +511,19 @@ int attnres_hip_packed_backward_noalloc(const void* values, int64_t source_strid
   if (2 * rank > kScratchElems)
     return fail(ATTNRES_ERR_WORKSPACE, "rank=%lld needs more than the %lld-element scratch", (long long)rank,
                 (long long)kScratchElems);
-  // the pointer checks of the workspace entry point, before any runtime call
+  // every argument check of the workspace entry point, before any runtime call
+  static const char* const kName = "attnres_hip_packed_backward_noalloc";
   if (!values || !query || (out_refine && !out) || !grad_out || !logit || !inv_rms || !stats || !grad_values ||
       !grad_query)
-    return fail(ATTNRES_ERR_NULL_POINTER, "null pointer argument to attnres_hip_packed_backward_noalloc");
+    return fail(ATTNRES_ERR_NULL_POINTER, "null pointer argument to %s", kName);
+  if ((st = check_recompute(!out_refine, n_sources, width, rank, kName))) return st;
+  if (source_stride < 0 || row_stride < 0) return fail(ATTNRES_ERR_STRIDE, "negative stride in %s", kName);
+  if ((st = check_scalars(1.0f, scale, false))) return st;
   float* workspace = nullptr;
   if ((st = device_scratch(&workspace))) return st;
   return packed_backward(values, source_stride, row_stride, n_sources, n_tokens, width, query, rank, scale, out,
                          out_refine, grad_out, logit, inv_rms, stats, grad_values, grad_query, workspace,
-                         kScratchElems, nullptr, false, stream, true);
+                         kScratchElems, nullptr, false, stream, true, kName);
 }
 
 int attnres_hip_packed_backward(const void* values, int64_t source_stride, int64_t row_stride,
@@ -610,7 +622,7 @@ int sources_backward(const void* const* sources, const int64_t* row_strides, int
       !inv_rms || !stats || (kCoef ? !coef : !grad_sources) || !grad_query || !dq_workspace ||
       (need_flags && !accumulate))
     return fail(ATTNRES_ERR_NULL_POINTER, "null pointer argument to %s", name);
-  if ((st = check_recompute(recompute, n_sources, name))) return st;
+  if ((st = check_recompute(recompute, n_sources, width, rank, name))) return st;
   if ((st = check_scalars(1.0f, scale, false))) return st;
   const int64_t need = workspace_elems(n_tokens, width, rank);
   if (dq_workspace_elems < need)

@@ -196,6 +196,29 @@ inline bool no_mask(const Geometry& geo, int64_t width, int64_t rank) {
   return rank == width && width == static_cast<int64_t>(geo.lanes) * geo.chunks * kVec;
 }
 
+// Key-resident backward (attnres_bwd_keyres_kernel): reads of more than
+// kRecomputeMaxSources and at most kKeyResMaxSources sources whose rows are
+// full 64-lane geometry rows (D = 64 * CH * 8) and whose key is the last
+// KC <= kKeyResMaxChunks whole chunk columns (R = KC * 512, R < D) save no
+// refinement either: the backward keeps the key chunks of a token's rows in
+// registers and takes delta from the value rows.  Returns KC, or 0 where the
+// kernel does not apply.
+constexpr int kKeyResMaxSources = ATTNRES_KEYRES_MAX_SOURCES;
+constexpr int kKeyResMaxChunks = 2;
+inline int keyres_key_chunks(int64_t D, int64_t R) {
+  const Geometry geo = geometry(D);
+  const int64_t column = static_cast<int64_t>(geo.lanes) * kVec;  // elements per chunk column
+  if (geo.lanes != 64 || D != geo.chunks * column || R >= D || R % column != 0) return 0;
+  const int64_t kc = R / column;
+  return kc <= kKeyResMaxChunks ? static_cast<int>(kc) : 0;
+}
+
+// Whether a read of S sources, width D and rank R can run its backward
+// without the saved output and refinement (the save/recompute policy).
+inline bool recomputes(int64_t S, int64_t D, int64_t R) {
+  return S <= kRecomputeMaxSources || (S <= kKeyResMaxSources && keyres_key_chunks(D, R) > 0);
+}
+
 // Lanes per token group of the recompute backward: it keeps S rows per lane,
 // so for the (64, 8) geometry (2048 < D <= 4096) it runs a whole workgroup
 // per token with 2 chunks per lane; every other geometry keeps its group.

@@ -43,7 +43,10 @@
 // Variants of the backward.  For S <= 6 (the save/recompute policy) a group
 // holds all S rows of its token and takes delta = sum_s p_s dw_s from them,
 // so the forward stores no refinement and the backward reads no saved output
-// (attnres_bwd_recompute_kernel).  The accumulating variant adds dv to
+// (attnres_bwd_recompute_kernel).  Reads of up to 16 sources whose key is a
+// suffix of whole chunk columns (R = 512 or 1024 of D = 2048 or 4096) do the
+// same while streaming their rows: only the key chunks of a token's rows are
+// held until delta is complete (attnres_bwd_keyres_kernel).  The accumulating variant adds dv to
 // existing gradient rows (BF16, or FP32 sums for a source bank).  The
 // coefficient variant writes no dv at all, only the per-token terms p, a, b;
 // a source bank later forms each source's gradient once from the dO rows of
@@ -1394,6 +1397,238 @@ __global__ void __launch_bounds__(kBlock) attnres_bwd_recompute_kernel(const Bwd
   store_dq_partial<G, CH>(dq, dq_lds, a.partial + static_cast<int64_t>(blockIdx.x) * R, group, lane, tail0, D);
 }
 
+// ------------------------------------------- backward, key-resident (R < D)
+
+// For a read whose key is a proper suffix of whole chunk columns (D = G*CH*8,
+// R = KC*G*8, KC < CH) of at most KS sources, the forward stores no
+// refinement and this backward reads neither the output nor its refinement,
+// like the recompute kernel, but it streams the value rows through a ring
+// instead of holding whole tokens.  Only the key coordinates of dv depend on
+// delta:
+//     dv_s = p_s dO  +  [key] (a_s q + b_s v_s),   a_s, b_s proportional to
+//     dz_s = p_s (dw_s - delta),  delta = sum_s p_s dw_s.
+// So each item stores the non-key part of its dv row (p_s dO) at once, adds
+// p_s dw_s to delta (in source order, as the recompute kernel does) and keeps
+// the key chunks of its value row in registers (KC chunks per source); after
+// the token's last item, delta is complete and the key part of every dv row
+// is formed from the held chunks.  The value rows are read once, the saved
+// output never: the backward moves its algorithmic bytes, and delta is the
+// exact FP32 sum instead of the refined BF16 output's.
+//
+// Group = one wavefront (G = 64).  Grid-stride over tokens like the streaming
+// kernel; NB value rows in flight in a ring that crosses token boundaries.
+// Items are counted per token with S rounded up to a multiple of NB (an item
+// past S loads the idle row and does nothing), so slot j always serves items
+// j, j + NB, ... and every register index is a compile-time constant.  The
+// next token's dO and statistics are requested two items before the token
+// ends.
+template <int G, int CH, int KC, int KS, int NB, bool LAG, bool VEC, class Rows, class Grads>
+__global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, 1)))
+attnres_bwd_keyres_kernel(const BwdArgs<Rows, Grads> a) {
+  static_assert(G == 64, "one wavefront per token group");
+  static_assert(KC >= 1 && KC < CH, "the key is a proper suffix of whole chunk columns");
+  static_assert(KS % NB == 0, "whole ring rounds per token");
+  static_assert(std::is_same_v<Grads, PackedGrads> || std::is_same_v<Grads, ListGrads>, "BF16 dv rows");
+  constexpr int C0 = CH - KC;  // first key chunk column
+  constexpr int kGroups = kBlock / G;
+  __shared__ float dq_lds[kGroups * G * kVec];
+  __shared__ __attribute__((aligned(16))) float q_lds[KC * G * kVec];
+  const int lane = threadIdx.x % G;
+  const int group = group_index<G>();
+  const int D = a.width;  // G * CH * 8
+  const int R = a.rank;   // KC * G * 8
+  const int S = a.n_sources;
+  const int Sp = (S + NB - 1) / NB * NB;
+  const float inv_R = 1.0f / static_cast<float>(R);
+  const float scale = a.scale;
+  int phase = 0;
+
+  for (int i = threadIdx.x; i < KC * G * kVec; i += kBlock) q_lds[i] = __uint_as_float(uint32_t{a.query[i]} << 16);
+  __syncthreads();
+  float dq[KC][kVec];
+#pragma unroll
+  for (int c = 0; c < KC; ++c)
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) dq[c][e] = 0.0f;
+
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * kGroups + group;
+  const int64_t groups = static_cast<int64_t>(gridDim.x) * kGroups;
+  const int64_t my_tokens = gid < a.n_tokens ? (a.n_tokens - 1 - gid) / groups + 1 : 0;
+
+  if (my_tokens > 0) {
+    int64_t token = gid;
+    u32x4 g[CH], pend_g[CH];
+    float run_max = a.stats[token], inv_sum = a.stats[a.n_tokens + token];
+    float pend_max = run_max, pend_sum = inv_sum;
+    load_row<G, CH, VEC>(a.grad_out + token * D, lane, D, g);
+    const uint16_t* idle = a.src.row(0, token);
+    u32x4 ring[NB][CH];
+    float ring_z[NB], ring_r[NB];
+    auto load_item = [&](int j, int64_t tok, int s, bool live) __attribute__((always_inline)) {
+      load_row<G, CH, VEC>(live ? a.src.row(s, tok) : idle, lane, D, ring[j]);
+      const int64_t item = live ? tok * S + s : 0;
+      ring_z[j] = a.logit[item];
+      ring_r[j] = a.inv_rms[item];
+    };
+#pragma unroll
+    for (int j = 0; j < NB; ++j) load_item(j, token, j, j < S);
+
+    // Held state of the previous token of the group: per source its key
+    // chunks and scalars, and the key chunks of its dO and its delta.
+    u32x4 key[KS][KC];
+    float kp[KS], kdw[KS], kz[KS], kr[KS];
+    constexpr int kHeldG = LAG ? CH : KC;  // chunks of the previous token's dO held: all, or the key's
+    u32x4 gprev[kHeldG];
+    float delta_prev = 0.0f;
+    int64_t prev = -1;  // none yet
+
+    // The key part of dv row (ss, prev) -- the previous token's delta is
+    // complete -- and its dq terms.
+    auto finish = [&](int ss) __attribute__((always_inline)) {
+      const float p = kp[ss];
+      const float dz = p * (kdw[ss] - delta_prev);
+      const float ca = kr[ss] * (dz * scale);
+      const float cb = -(kr[ss] * kr[ss]) * (dz * kz[ss] * inv_R);
+      uint16_t* grad_row = a.grad.row(ss, prev, D);
+      if constexpr (LAG) {  // the non-key part too: one whole-row store
+#pragma unroll
+        for (int c = 0; c < C0; ++c) {
+          const uint32_t gw[4] = {gprev[c].x, gprev[c].y, gprev[c].z, gprev[c].w};
+          uint32_t out[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) out[k] = pack_bf16x2(p * bf16_lo(gw[k]), p * bf16_hi(gw[k]));
+          store_chunk<G, VEC>(grad_row, chunk_start<G>(c, lane), D, u32x4{out[0], out[1], out[2], out[3]});
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < KC; ++c) {
+        const uint32_t w[4] = {key[ss][c].x, key[ss][c].y, key[ss][c].z, key[ss][c].w};
+        u32x4 gk;
+        if constexpr (LAG) {
+          gk = gprev[C0 + c];
+        } else {
+          gk = gprev[c];
+        }
+        const uint32_t gw[4] = {gk.x, gk.y, gk.z, gk.w};
+        const float4 qa = *reinterpret_cast<const float4*>(&q_lds[(c * G + lane) * kVec]);
+        const float4 qb = *reinterpret_cast<const float4*>(&q_lds[(c * G + lane) * kVec + 4]);
+        const float qf[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+        uint32_t out[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float k0 = bf16_lo(w[k]), k1 = bf16_hi(w[k]);
+          const float v0 = fmaf(cb, k0, fmaf(ca, qf[2 * k], p * bf16_lo(gw[k])));
+          const float v1 = fmaf(cb, k1, fmaf(ca, qf[2 * k + 1], p * bf16_hi(gw[k])));
+          dq[c][2 * k] = fmaf(ca, k0, dq[c][2 * k]);
+          dq[c][2 * k + 1] = fmaf(ca, k1, dq[c][2 * k + 1]);
+          out[k] = pack_bf16x2(v0, v1);
+        }
+        store_chunk<G, VEC>(grad_row, chunk_start<G>(C0 + c, lane), D, u32x4{out[0], out[1], out[2], out[3]});
+      }
+    };
+
+    // Item ss of a token also finishes source ss of the group's previous
+    // token (both have S items), so the key-part work is spread over the
+    // stream instead of bunching at each token's end.
+    for (int64_t ti = 0; ti < my_tokens; ++ti) {
+      const bool more = ti + 1 < my_tokens;
+      const int64_t next = token + groups;
+      const int request_at = S > 2 ? S - 2 : 0;
+      float delta = 0.0f;
+#pragma unroll
+      for (int ss = 0; ss < KS; ++ss) {
+        if (ss >= Sp) continue;  // uniform; a constant trip count keeps every register index static
+        const int j = ss % NB;
+        float p = 0.0f, dw[1] = {0.0f};
+        u32x4 held[KC];
+        if (ss < S) {
+          {
+            float dw1 = 0.0f;
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+              dw[0] = dot2(ring[j][c].x, g[c].x, dw[0]);
+              dw1 = dot2(ring[j][c].y, g[c].y, dw1);
+              dw[0] = dot2(ring[j][c].z, g[c].z, dw[0]);
+              dw1 = dot2(ring[j][c].w, g[c].w, dw1);
+            }
+            dw[0] += dw1;
+          }
+          group_sum<G, 1>(dw, nullptr, phase);  // G = 64: wavefront sums, no LDS
+          p = __expf(ring_z[j] - run_max) * inv_sum;
+          delta = fmaf(p, dw[0], delta);
+          if constexpr (!LAG) {  // the non-key part of this item's dv row now
+            uint16_t* grad_row = a.grad.row(ss, token, D);
+#pragma unroll
+            for (int c = 0; c < C0; ++c) {
+              const uint32_t gw[4] = {g[c].x, g[c].y, g[c].z, g[c].w};
+              uint32_t out[4];
+#pragma unroll
+              for (int k = 0; k < 4; ++k) out[k] = pack_bf16x2(p * bf16_lo(gw[k]), p * bf16_hi(gw[k]));
+              store_chunk<G, VEC>(grad_row, chunk_start<G>(c, lane), D, u32x4{out[0], out[1], out[2], out[3]});
+            }
+          }
+#pragma unroll
+          for (int c = 0; c < KC; ++c) held[c] = ring[j][C0 + c];
+        }
+        const float z_now = ring_z[j], r_now = ring_r[j];  // the refill below replaces them
+        if (more && ss == request_at) {
+          load_row<G, CH, VEC>(a.grad_out + next * D, lane, D, pend_g);
+          pend_max = a.stats[next];
+          pend_sum = a.stats[a.n_tokens + next];
+        }
+        __builtin_amdgcn_sched_barrier(0);  // refill the slot after its last use
+        const int sn = ss + NB;
+        if (sn < Sp) {
+          load_item(j, token, sn, sn < S);
+        } else {
+          load_item(j, next, sn - Sp, more && sn - Sp < S);
+        }
+        if (ss < S) {
+          if (prev >= 0) finish(ss);  // uniform
+#pragma unroll
+          for (int c = 0; c < KC; ++c) key[ss][c] = held[c];
+          kp[ss] = p;
+          kdw[ss] = dw[0];
+          kz[ss] = z_now;
+          kr[ss] = r_now;
+        }
+      }
+      delta_prev = delta;
+#pragma unroll
+      for (int c = 0; c < kHeldG; ++c) gprev[c] = g[LAG ? c : C0 + c];
+      prev = token;
+      if (more) {
+#pragma unroll
+        for (int c = 0; c < CH; ++c) g[c] = pend_g[c];
+        run_max = pend_max;
+        inv_sum = pend_sum;
+      }
+      token = next;
+    }
+#pragma unroll
+    for (int ss = 0; ss < KS; ++ss) {
+      if (ss < S) finish(ss);  // the group's last token
+    }
+  }
+
+  // this block's dq partial row (key coordinates only; R = KC * G * 8), the
+  // groups summed in a fixed order
+  float* partial = a.partial + static_cast<int64_t>(blockIdx.x) * R;
+#pragma unroll
+  for (int c = 0; c < KC; ++c) {
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) dq_lds[group * (G * kVec) + lane * kVec + e] = dq[c][e];
+    __syncthreads();
+    for (int j = threadIdx.x; j < G * kVec; j += kBlock) {
+      float t = dq_lds[j];
+#pragma unroll
+      for (int k = 1; k < kGroups; ++k) t += dq_lds[k * (G * kVec) + j];
+      partial[c * G * kVec + j] = t;
+    }
+    __syncthreads();
+  }
+}
+
 // ---------------------------------------------------------- source-bank gather
 
 // The gradient of one source-bank slot, gathered from the reads that saw it:
@@ -1823,12 +2058,54 @@ int64_t launch_bwd_recompute(const BwdArgs<Rows, Grads>& a, hipStream_t stream) 
   return launch_bwd_recompute_rows<G, CH, kRecomputeMaxSources, NOMASK, VEC>(a, stream);
 }
 
+// The key-resident backward for reads of kRecomputeMaxSources < S <=
+// kKeyResMaxSources whose key is KC = keyres_key_chunks(D, R) whole chunk
+// columns (the host checks this before choosing the recompute path).
+// Two rows in flight per group (four were slower or spilled); rows of 4096
+// (8 chunks per lane) write each dv row whole, one token later (LAG).
+// Measured on MI355X (fwd + bwd per read, us; saved refinement -> key-resident
+// with the key part one token later -> whole rows one token later):
+// S = 16, N = 16384, D = 4096, R = 1024 (c3): 1207.8 -> 1207.1 -> 1198.7;
+// S = 9, D = 4096, R = 1024: 734.7 -> 713.7 -> 713.1; S = 13, D = 4096,
+// R = 512: 1011.9 -> 998.3 -> 1000.7; S = 9, N = 32768, D = 2048, R = 1024:
+// 723.6 -> 708.1 -> 715.7; S = 16, D = 2048, R = 512: 598.9 -> 594.1 ->
+// 591.4.  The forward, which stores no refinement, gains most of it
+// (c3: 390 -> 372 us); the backward moves 4% fewer bytes at about the same
+// time.  A first version that formed every key part at the token's end (two
+// rows in flight over that burst) took 862 us for the c3 backward.
+template <int G, int CH, int KC, bool VEC, class Rows, class Grads>
+int64_t launch_bwd_keyres_chunks(const BwdArgs<Rows, Grads>& a, hipStream_t stream) {
+  constexpr int NB = 2;
+  constexpr bool LAG = CH == 8;
+  const int64_t resident =
+      resident_blocks<&attnres_bwd_keyres_kernel<G, CH, KC, kKeyResMaxSources, NB, LAG, VEC, Rows, Grads>>();
+  const int64_t blocks = grid_blocks(a.n_tokens, G, kBwdGridPerResident * resident, a.max_grid);
+  hipLaunchKernelGGL((attnres_bwd_keyres_kernel<G, CH, KC, kKeyResMaxSources, NB, LAG, VEC, Rows, Grads>),
+                     dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream, a);
+  return blocks;
+}
+
+template <int G, int CH, class Rows, class Grads>
+int64_t launch_bwd_keyres(const BwdArgs<Rows, Grads>& a, bool vec, hipStream_t stream) {
+  if constexpr (G == 64 && CH > kKeyResMaxChunks) {
+    switch (keyres_key_chunks(a.width, a.rank)) {
+      case 1: return vec ? launch_bwd_keyres_chunks<G, CH, 1, true>(a, stream)
+                         : launch_bwd_keyres_chunks<G, CH, 1, false>(a, stream);
+      case 2: return vec ? launch_bwd_keyres_chunks<G, CH, 2, true>(a, stream)
+                         : launch_bwd_keyres_chunks<G, CH, 2, false>(a, stream);
+      default: break;
+    }
+  }
+  return 0;  // not reached: the host accepts such reads only where keyres_key_chunks applies
+}
+
 // The recompute kernel keeps S rows per lane: for the (64, 8) geometry
 // (2048 < D <= 4096) it runs with a whole workgroup per token instead, two
 // chunks per lane (same lane positions covered, so the same NOMASK rule);
 // its grid counts those groups (one token per workgroup).
 template <int G, int CH, class Rows, class Grads>
 int64_t launch_bwd_recompute_geometry(const BwdArgs<Rows, Grads>& a, bool nomask, bool vec, hipStream_t stream) {
+  if (a.n_sources > kRecomputeMaxSources) return launch_bwd_keyres<G, CH>(a, vec, stream);
   constexpr int RG = recompute_lanes(G, CH);
   constexpr int RCH = G * CH / RG;
   static_assert(RG * RCH == G * CH, "same row coverage");

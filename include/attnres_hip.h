@@ -19,6 +19,10 @@
  *     HIP include); work is only enqueued on it: nothing here allocates,
  *     synchronises or reads device memory from the host, so every call may be
  *     captured into a HIP graph;
+ *   - calls share no mutable state, except attnres_hip_packed_backward_noalloc,
+ *     whose calls on one GPU share its device scratch array: two of them that
+ *     overlap in time there (concurrent streams or threads, or two captured
+ *     graphs replayed at once) race;
  *   - the return value is ATTNRES_OK or one of the codes below; arguments are
  *     fully checked on the host before anything is enqueued, so an invalid
  *     call never launches a kernel.  attnres_hip_last_error() describes the
@@ -40,9 +44,13 @@
  * sources need not save the output's refinement: pass out_refine = NULL to
  * the forward (nothing is stored) and out = out_refine = NULL to the plain
  * backward, which then derives delta = <dO, o> = sum_s p_s <v_s, dO> from
- * the value rows it reads anyway.  Larger reads must save it.  (The reference
- * makes the same structural choice with a threshold of 3: recompute for
- * S <= 3, save the FP32 mixed output for S >= 4,
+ * the value rows it reads anyway.  So need reads of at most
+ * ATTNRES_KEYRES_MAX_SOURCES whose rows are 2048 or 4096 elements wide and
+ * whose key is their last 512 or 1024 (the key-resident backward keeps the
+ * key coordinates of a token's rows in registers while the rows stream by).
+ * attnres_hip_saves_refinement_for tells them apart; other reads must save
+ * it.  (The reference makes the same structural choice with a threshold of
+ * 3: recompute for S <= 3, save the FP32 mixed output for S >= 4,
  * src/attnres/_kernels/fla_full_sources.py:146-161.  Here the recompute
  * backward holds a token's rows in registers, which pays up to 6 sources.)
  */
@@ -70,6 +78,9 @@ enum attnres_status {
 #define ATTNRES_MAX_WIDTH 8192
 /* Reads of at most this many sources may skip the refinement (see above). */
 #define ATTNRES_RECOMPUTE_MAX_SOURCES 6
+/* The key-resident backward takes reads of up to this many sources (see
+ * attnres_hip_saves_refinement_for). */
+#define ATTNRES_KEYRES_MAX_SOURCES 16
 
 /* Element types of attnres_hip_partial_sum and attnres_hip_bank_gather. */
 #define ATTNRES_DTYPE_F32 0
@@ -88,8 +99,23 @@ const char* attnres_hip_last_error(void);
  * 1 = save (the forward stores out_refine, the backward reads out and
  * out_refine), 0 = recompute (n_sources <= ATTNRES_RECOMPUTE_MAX_SOURCES).
  * Host-only.  Replaces `_should_save_mixed` (fla_full_sources.py:146-161).
+ * Reads of more sources may recompute too, depending on their shape: see
+ * attnres_hip_saves_refinement_for.
  */
 int attnres_hip_saves_refinement(int64_t n_sources);
+
+/*
+ * The save/recompute policy for a read of the given shape: 0 (recompute) for
+ * n_sources <= ATTNRES_RECOMPUTE_MAX_SOURCES, and also for
+ * n_sources <= ATTNRES_KEYRES_MAX_SOURCES when the rows are 2048 or 4096
+ * elements wide and the key is their last 512 or 1024 (the key-resident
+ * backward: it holds the key coordinates of a token's rows and takes delta
+ * from the value rows); 1 (save) otherwise.  The forward of a recomputing
+ * read may pass out_refine = NULL, and its backward must then get
+ * out = out_refine = NULL.  Host-only.  Replaces `_should_save_mixed`
+ * (fla_full_sources.py:146-161), which keys on the source count alone.
+ */
+int attnres_hip_saves_refinement_for(int64_t n_sources, int64_t width, int64_t rank);
 
 /*
  * Packed forward.  values[s, n, :] lives at values + s*source_stride +
@@ -123,8 +149,9 @@ int64_t attnres_hip_dq_workspace_elems(int64_t n_tokens, int64_t width,
  * BF16) and the saved statistics; writes grad_values[S, N, D] (contiguous BF16) and
  * grad_query[R] (BF16).  dq is reduced over all tokens in a fixed order, so it
  * is bit-identical from run to run.  out_refine = NULL (and out ignored, may
- * be NULL) selects the recompute kernel: n_sources must then be at most
- * ATTNRES_RECOMPUTE_MAX_SOURCES (else ATTNRES_ERR_SHAPE).
+ * be NULL) selects the recompute or key-resident kernel: the read must then
+ * be one that attnres_hip_saves_refinement_for says need not save (else
+ * ATTNRES_ERR_SHAPE).
  *
  * Replaces `attnres::_fixed_tail_backward` (fixed_tail.py:962-1034):
  * `_packed_online_backward_kernel` (fixed_tail.py:485-873) plus
@@ -153,8 +180,12 @@ int attnres_hip_packed_backward(const void* values, int64_t source_stride,
  * workgroups: dv is the same bits, dq may differ in the FP32 order of its
  * partial sums.  rank must be at most 2^19 (always so within the envelope),
  * else ATTNRES_ERR_WORKSPACE.  Calls on one GPU share that array, so calls
- * that overlap in time on one GPU (concurrent streams, threads) race; calls
- * in stream order do not.
+ * that overlap in time on one GPU (concurrent streams, threads, or two
+ * graphs captured with it replayed at once) race; calls in stream order do
+ * not.  The first call on each device looks the array up
+ * (hipGetSymbolAddress): make it outside stream capture; later calls make
+ * only the runtime calls of every entry point (hipGetDevice, the occupancy
+ * queries cached per kernel, the launches) and may be captured.
  *
  * No counterpart in the reference (its backward allocates dq partials with
  * torch.empty, fixed_tail.py:980-984).  For callers that cannot allocate

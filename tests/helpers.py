@@ -45,6 +45,7 @@ oracle, max ulps against the oracle and against float64); with
 from __future__ import annotations
 
 import torch
+from torch.utils._python_dispatch import TorchDispatchMode
 
 from oracle.oracle import BF16_TOLERANCE, exact_with_grads, oracle, oracle_float64, softmax_statistics
 
@@ -56,12 +57,12 @@ STAT_RTOL = 1e-5       # saved statistics: relative tolerance (north_star)
 DELTA_SIGMAS = 6.0     # saved-output reads: standard deviations of the delta error allowed
 
 
-def saves_output(sources: int) -> bool:
-    """Whether a read of ``sources`` sources saves its output and refinement
-    (its backward takes delta from them) under the product's policy."""
+def saves_output(sources: int, width: int, rank: int) -> bool:
+    """Whether a read of this shape saves its output and refinement (its
+    backward takes delta from them) under the product's policy."""
     from attnres._ops import saves_refinement
 
-    return saves_refinement(sources)
+    return saves_refinement(sources, width, rank)
 
 
 def delta_allowance(packed: torch.Tensor, query: torch.Tensor, upstream: torch.Tensor, *,
@@ -271,7 +272,9 @@ def compare_read(actual, expected, exact, names=None, *, sources: int | None = N
     gradient ("dq") get the `delta_allowance` that `exact_grads` attached to
     their float64 gradient."""
     names = names or ["out"] + [f"grad{i}" for i in range(len(actual) - 1)]
-    saved = sources is not None and saves_output(sources)
+    width = int(actual[0].shape[-1])
+    rank = int(actual[names.index("dq")].numel()) if "dq" in names else width
+    saved = sources is not None and saves_output(sources, width, rank)
     metrics = []
     for a, e, x, n in zip(actual, expected, exact, names):
         extra = None
@@ -336,6 +339,48 @@ def both_oracles(make_values, leaves, query_leaf, upstream, *, eps=2**-23, scale
     return (out, *grads), (out64, *grads64)
 
 
+# ------------------------------------------------------ accumulated gradients
+
+def accumulated_bound(per_read: list, allowances: list, roundings: int, floor: float = FLOOR) -> torch.Tensor:
+    """Per-element bound on |result - exact| for a gradient summed over reads.
+
+    ``per_read``: each read's exact (float64) contribution to the gradient;
+    ``allowances``: each read's `delta_allowance` on it (None for a read that
+    takes delta from the value rows); ``roundings``: how many times the
+    running sum is rounded to BF16 (the accumulating BF16 backward rounds once
+    per read; FP32 sums never; a BF16 store of an FP32 sum once).  Each
+    rounding of a partial sum is at most half an ulp of it, and every partial
+    sum is at most the sum of the reads' absolute contributions, so the
+    roundings add at most ``roundings / 2`` ulps of that; each read adds its
+    FP32 arithmetic (the ``floor`` times its own row maximum, as for a single
+    read) and its delta allowance."""
+    magnitude = sum(d.abs() for d in per_read)
+    bound = 0.5 * roundings * bf16_ulp(magnitude)
+    for d in per_read:
+        bound = bound + _row_floor(d, floor)
+    for extra in allowances:
+        if extra is not None:
+            bound = bound + extra
+    return bound
+
+
+def check_accumulated(actual: torch.Tensor, exact: torch.Tensor, bound: torch.Tensor, name: str) -> float:
+    """Assert |actual - exact| <= bound element by element; return the largest
+    ratio of the error to the bound (recorded under the current case)."""
+    a = actual.detach().cpu().double()
+    x = exact.detach().cpu().double()
+    assert torch.isfinite(a).all(), f"{name}: non-finite result"
+    error = (a - x).abs()
+    ratio = error / bound.clamp_min(TINY)
+    worst = float(ratio.max()) if ratio.numel() else 0.0
+    RECORDS.append({"case": _CASE[0], "tensor": name, "accumulated_bound_ratio": worst})
+    if worst > 1.0:
+        index = tuple(int(i) for i in torch.unravel_index(ratio.argmax(), ratio.shape))
+        raise AssertionError(f"{name}: error {float(error[index]):.4g} at {index} is {worst:.3g} x its bound "
+                             f"{float(bound[index]):.4g} (result {float(a[index]):.6g}, exact {float(x[index]):.6g})")
+    return worst
+
+
 # ------------------------------------------------------------- statistics
 
 def kernel_statistics(values, query, eps, scale):
@@ -391,7 +436,36 @@ def check_statistics(values, query, *, eps=2**-23, scale=1.0, chunk: int = 4096)
     return worst
 
 
-__all__ = ["DELTA_SIGMAS", "FLOOR", "RECORDS", "SEEDS", "STAT_RTOL", "Streamed", "both_oracles", "bf16_ulp",
+# ------------------------------------------------------- no source stack
+
+class SourceStackGuard(TorchDispatchMode):
+    """Fails on ``aten.stack`` / ``aten.cat`` of the read's sources: a list of
+    ``count`` (or ``count + 1``) tensors, all of one of the sources' shapes
+    (or that shape with a leading 1)."""
+
+    def __init__(self, shapes, count):
+        super().__init__()
+        self.shapes = {tuple(shape) for shape in shapes}
+        self.counts = {count, count + 1}
+        self.seen = 0
+
+    @classmethod
+    def ignore_compile_internals(cls):
+        return True  # watch the compiled artefact, not dynamo's own tracing
+
+    def _is_source(self, shape):
+        return shape in self.shapes or (len(shape) > 1 and shape[0] == 1 and shape[1:] in self.shapes)
+
+    def __torch_dispatch__(self, func, types, args=(), kwargs=None):
+        self.seen += 1
+        if func in (torch.ops.aten.stack.default, torch.ops.aten.cat.default) and args and args[0]:
+            shapes = [tuple(t.shape) for t in args[0]]
+            if len(shapes) in self.counts and len(set(shapes)) == 1 and self._is_source(shapes[0]):
+                raise AssertionError(f"the source-list path stacked its sources ({func})")
+        return func(*args, **(kwargs or {}))
+
+
+__all__ = ["DELTA_SIGMAS", "FLOOR", "RECORDS", "SEEDS", "STAT_RTOL", "SourceStackGuard", "Streamed", "accumulated_bound", "check_accumulated", "both_oracles", "bf16_ulp",
            "check_statistics", "delta_allowance", "saves_output", "worst_element",
            "compare", "compare_read", "exact_grads", "exact_with_grads", "kernel_statistics", "oracle_grads",
            "set_case", "ulp_error"]

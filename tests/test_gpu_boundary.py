@@ -21,10 +21,9 @@ import weakref
 
 import pytest
 import torch
-from torch.utils._python_dispatch import TorchDispatchMode
 
 from attnres import attnres
-from helpers import SEEDS, both_oracles, compare_read, set_case
+from helpers import SEEDS, SourceStackGuard, both_oracles, compare_read, set_case
 from oracle.oracle import oracle
 
 pytestmark = pytest.mark.gpu
@@ -152,33 +151,6 @@ def test_non_affine_output_batches_keep_every_gradient(rank, sequence):
 
 # --------------------------------------------------------- no source stack
 
-class _SourceStackGuard(TorchDispatchMode):
-    """Fails on ``aten.stack`` / ``aten.cat`` of the read's sources: a list of
-    ``count`` (or ``count + 1``) tensors, all of one of the sources' shapes
-    (or that shape with a leading 1)."""
-
-    def __init__(self, shapes, count):
-        super().__init__()
-        self.shapes = {tuple(shape) for shape in shapes}
-        self.counts = {count, count + 1}
-        self.seen = 0
-
-    @classmethod
-    def ignore_compile_internals(cls):
-        return True  # watch the compiled artefact, not dynamo's own tracing
-
-    def _is_source(self, shape):
-        return shape in self.shapes or (len(shape) > 1 and shape[0] == 1 and shape[1:] in self.shapes)
-
-    def __torch_dispatch__(self, func, types, args=(), kwargs=None):
-        self.seen += 1
-        if func in (torch.ops.aten.stack.default, torch.ops.aten.cat.default) and args and args[0]:
-            shapes = [tuple(t.shape) for t in args[0]]
-            if len(shapes) in self.counts and len(set(shapes)) == 1 and self._is_source(shapes[0]):
-                raise AssertionError(f"the source-list path stacked its sources ({func})")
-        return func(*args, **(kwargs or {}))
-
-
 def _list_inputs(count, tokens, width, rank):
     torch.manual_seed(SEEDS[2])
     leaves = [torch.randn(tokens, width, device="cuda", dtype=torch.bfloat16, requires_grad=True)
@@ -201,7 +173,7 @@ def test_list_path_never_stacks_its_sources(count, compiled):
     function = torch.compile(read, fullgraph=True, dynamic=False) if compiled else read
     if compiled:  # compile outside the guard, then run the artefact under it
         function(*leaves, query)
-    guard = _SourceStackGuard([leaf.shape for leaf in leaves], count)
+    guard = SourceStackGuard([leaf.shape for leaf in leaves], count)
     with guard:
         out = function(*leaves, query)
         grads = torch.autograd.grad(out, (*leaves, query), upstream)
@@ -216,5 +188,5 @@ def test_the_guard_catches_a_stacked_read():
     leaves = [torch.randn(7, 16, dtype=torch.bfloat16) for _ in range(3)]
     query = torch.randn(16, dtype=torch.bfloat16)
     with pytest.raises(AssertionError, match="stacked its sources"):
-        with _SourceStackGuard([leaf.shape for leaf in leaves], 3):
+        with SourceStackGuard([leaf.shape for leaf in leaves], 3):
             oracle(tuple(leaves), query)

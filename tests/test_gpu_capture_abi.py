@@ -133,3 +133,63 @@ def test_abi_calls_replay_from_a_hip_graph(layout):
             hip.hipGraphExecDestroy(exec_)
         if graph.value:
             hip.hipGraphDestroy(graph)
+
+
+@pytest.mark.parametrize("shape", [(25, 4096, 2048, 2048), (5, 515, 1024, 384)], ids=lambda s: "x".join(map(str, s)))
+def test_no_alloc_backward_replays_from_a_hip_graph(shape):
+    """The no-allocation backward under stream capture: its first call on the
+    device (which looks up the library's scratch array) is made eagerly, then
+    a call is captured and the graph replayed on changed upstream gradients;
+    every replay must equal an eager call on the same inputs bit for bit.
+    The saved-refinement path (S = 25) and the recompute path (S = 5)."""
+    hip = _hip_runtime()
+    lib = _native.load()
+    sources, tokens, width, rank = shape
+    torch.manual_seed(11)
+    dev = "cuda"
+    values = torch.randn(sources, tokens, width, device=dev).to(torch.bfloat16)
+    query = (torch.randn(rank, device=dev) / math.sqrt(rank)).to(torch.bfloat16)
+    grad_out = torch.randn(tokens, width, device=dev).to(torch.bfloat16)
+    from attnres import _ops
+
+    saved = _ops.saves_refinement(sources, width, rank)
+    out, refine, logit, inv_rms, stats = _ops.packed_forward_impl(values, query, 2**-23, 1.0, saved)
+    dv = torch.empty_like(values)
+    dq = torch.empty(rank, device=dev, dtype=torch.bfloat16)
+    side = torch.cuda.Stream()
+    handle = side.cuda_stream
+
+    def call():
+        st = lib.attnres_hip_packed_backward_noalloc(
+            values.data_ptr(), tokens * width, width, sources, tokens, width, query.data_ptr(), rank, 1.0,
+            out.data_ptr() if saved else None, refine.data_ptr() if saved else None, grad_out.data_ptr(),
+            logit.data_ptr(), inv_rms.data_ptr(), stats.data_ptr(), dv.data_ptr(), dq.data_ptr(), handle)
+        assert st == 0, lib.attnres_hip_last_error()
+
+    print(f"no-alloc capture S,N,D,R={shape}", flush=True)
+    torch.cuda.synchronize()
+    call()  # first call on the device, outside capture
+    assert hip.hipStreamSynchronize(handle) == 0
+    graph, exec_ = ctypes.c_void_p(), ctypes.c_void_p()
+    assert hip.hipStreamBeginCapture(handle, _CAPTURE_MODE_RELAXED) == 0
+    call()
+    assert hip.hipStreamEndCapture(handle, ctypes.byref(graph)) == 0
+    try:
+        assert hip.hipGraphInstantiate(ctypes.byref(exec_), graph, None, None, 0) == 0
+        for replay in range(3):
+            with torch.cuda.stream(side):
+                grad_out.copy_(torch.randn(tokens, width, device=dev).to(torch.bfloat16))
+            call()  # eager on the new inputs
+            assert hip.hipStreamSynchronize(handle) == 0
+            eager = (dv.clone(), dq.clone())
+            with torch.cuda.stream(side):
+                dv.zero_()
+                dq.zero_()
+            assert hip.hipGraphLaunch(exec_, handle) == 0
+            assert hip.hipStreamSynchronize(handle) == 0
+            assert torch.equal(dv, eager[0]) and torch.equal(dq, eager[1]), f"replay {replay}"
+    finally:
+        if exec_.value:
+            hip.hipGraphExecDestroy(exec_)
+        if graph.value:
+            hip.hipGraphDestroy(graph)

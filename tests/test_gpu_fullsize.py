@@ -74,7 +74,7 @@ def _check_full(values, query, upstream, *, listed, chunk=2048, exact_all=True):
     out, dv, dq = _read(flat, query, g, listed)
     torch.cuda.synchronize()
     sources = len(values) if listed else int(values.shape[0])
-    saved = saves_output(sources)
+    saved = saves_output(sources, width, int(query.numel()))
     out_check, dv_check = Streamed("out"), Streamed("dv", allowance=saved)
     dq32 = dq64 = None
     dq_variance = torch.zeros(int(query.numel()), dtype=torch.float64)
@@ -155,14 +155,62 @@ def test_block_list_config_every_row_matches_oracle():
     _independent_sample(sources, queries[0], upstreams[0], True, out, dv)
 
 
+@pytest.mark.parametrize("sources", _C5_SOURCES)
 @pytest.mark.parametrize("width,rank", [(1024, 1024), (1024, 256), (4096, 4096), (4096, 1024)],
                          ids=lambda v: str(v))
-def test_sweep_subset_matches_oracle(width, rank):
+def test_sweep_subset_matches_oracle(width, rank, sources):
+    """One read of the c5 subset per test (its rows are the first S sources of
+    the sweep's [48, N, D] input), so that no single test runs for minutes."""
     tokens = bench.CONFIGS["c5"]["batch"][0]
     values, query, upstream = bench.make_inputs(dict(sources=max(_C5_SOURCES), batch=(tokens,), width=width,
                                                      rank=rank), "cuda", seed=width + rank)
-    for sources in _C5_SOURCES:
-        print(f"c5 subset S={sources} N={tokens} D={width} R={rank}", flush=True)
-        set_case(f"c5 S={sources} D={width} R={rank}")
-        _check_full(values[:sources], query, upstream, listed=False, chunk=2048 if width <= 1024 else 1024,
-                    exact_all=False)
+    print(f"c5 subset S={sources} N={tokens} D={width} R={rank}", flush=True)
+    set_case(f"c5 S={sources} D={width} R={rank}")
+    _check_full(values[:sources], query, upstream, listed=False,
+                chunk=2048 if width <= 1024 else 1024, exact_all=False)
+
+
+def test_block_list_three_shared_reads_full_size():
+    """c4 as its step runs it: the three reads of the 9 shared sources through
+    `SharedSources`, whose backward adds each read's dv to the sources'
+    gradients inside the kernel.  Every row of every source's summed gradient
+    against the exact sum of the three reads' float64 gradients, within
+    `helpers.accumulated_bound` (three BF16 roundings, each read's FP32 floor
+    and delta allowance); every output row within one ulp of float64; each
+    query's gradient within one ulp of float64 plus its allowance."""
+    from attnres import SharedSources
+    from helpers import DELTA_SIGMAS, accumulated_bound, check_accumulated, exact_grads, ulp_error
+
+    cfg = bench.CONFIGS["c4"]
+    print(f"full size c4, three shared reads: {cfg['name']}", flush=True)
+    set_case("c4 full size, three shared reads")
+    sources, queries, upstreams = bench.make_block_sources(cfg, "cuda", seed=0)
+    leaves = [s.requires_grad_() for s in sources]
+    queries = [q.requires_grad_() for q in queries]
+    bank = SharedSources(leaves)
+    outs = [bank.read(q) for q in queries]
+    results = torch.autograd.grad(sum((o.float() * g.float()).sum() for o, g in zip(outs, upstreams)),
+                                  (*leaves, *queries))
+    torch.cuda.synchronize()
+    count, tokens = len(leaves), int(leaves[0].shape[0])
+    make = lambda ls, q: (tuple(ls), q)  # noqa: E731
+    dq_exact = [0.0] * len(queries)
+    dq_variance = [0.0] * len(queries)
+    worst = 0.0
+    for start in range(0, tokens, 2048):
+        stop = min(tokens, start + 2048)
+        rows = [leaf[start:stop] for leaf in leaves]
+        per_read = [exact_grads(make, rows, q, g[start:stop]) for q, g in zip(queries, upstreams)]
+        for r, (out64, grads64) in enumerate(per_read):
+            assert ulp_error(outs[r][start:stop], out64) <= 1.0, f"read {r} output rows {start}..{stop}"
+            dq_exact[r] = dq_exact[r] + grads64[count]
+            dq_variance[r] = dq_variance[r] + (grads64[count].dq_allowance / DELTA_SIGMAS) ** 2
+        for i in range(count):
+            contributions = [grads64[i] for _, grads64 in per_read]
+            bound = accumulated_bound(contributions, [c.dv_allowance for c in contributions], roundings=len(per_read))
+            worst = max(worst, check_accumulated(results[i][start:stop], sum(contributions), bound,
+                                                 f"source {i} rows {start}..{stop}"))
+    print(f"  worst error / bound over every source row: {worst:.3f}", flush=True)
+    for r in range(len(queries)):
+        allowance = DELTA_SIGMAS * dq_variance[r].sqrt()
+        assert ulp_error(results[count + r], dq_exact[r], extra=allowance) <= 1.0, f"dq of read {r}"

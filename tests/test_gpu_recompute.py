@@ -113,3 +113,94 @@ def test_recompute_special_cases_are_exact():
     assert torch.equal(out, twin[0])
     assert torch.equal(dv, (upstream.float() / 2).to(torch.bfloat16).expand(2, -1, -1))
     assert torch.count_nonzero(dq) == 0
+
+
+# The key-resident backward (`attnres_bwd_keyres_kernel`): reads of 7..16
+# sources whose rows are 2048 or 4096 elements wide and whose key is their last
+# 512 or 1024 elements save no refinement either; the backward keeps the key
+# chunks of a token's rows in registers and takes delta from the value rows.
+KEYRES_SHAPES = [(2048, 512), (2048, 1024), (4096, 512), (4096, 1024)]
+
+
+@pytest.mark.parametrize("layout", ["packed", "list"])
+@pytest.mark.parametrize("padded", [False, True], ids=["aligned", "padded"])
+@pytest.mark.parametrize("width,rank", KEYRES_SHAPES, ids=lambda v: str(v))
+@pytest.mark.parametrize("sources", [7, 8, 13, 16])
+def test_key_resident_backward_matches_oracle(sources, width, rank, padded, layout):
+    """Against the oracle at the full bars with no delta allowance: delta is
+    an FP32 sum over the value rows, not the refined BF16 output.  Padded rows
+    (7 elements of padding) take the element-wise path."""
+    assert not _ops.saves_refinement(sources, width, rank)
+    tokens = 37
+    producer, query, upstream = _inputs(sources, tokens, width, rank, padded, SEEDS[0] + 3 * width + sources)
+
+    def make(leaves, q):
+        values = leaves[0][..., :width]
+        return (tuple(values.unbind(0)) if layout == "list" else values), q
+
+    print(f"key-resident S={sources} D={width} R={rank} padded={padded} layout={layout}", flush=True)
+    set_case(f"key-resident S={sources} D={width} R={rank} padded={padded} {layout}")
+    actual = attnres(make([producer], query)[0], query)
+    grads = torch.autograd.grad(actual, (producer, query), upstream)
+    expected, exact = both_oracles(make, [producer], query, upstream)
+    torch.cuda.synchronize()
+    compare_read((actual, *grads), expected, exact, ["out", "dv", "dq"], sources=sources)
+    check_statistics(make([producer.detach()], query)[0], query.detach())
+
+
+@pytest.mark.parametrize("layout", ["packed", "list"])
+@pytest.mark.parametrize("width,rank", KEYRES_SHAPES, ids=lambda v: str(v))
+@pytest.mark.parametrize("sources,tokens", [(7, 5003), (16, 2053), (9, 1)], ids=lambda v: str(v))
+def test_key_resident_agrees_with_the_saved_refinement_path(sources, tokens, width, rank, layout):
+    """Same inputs through the key-resident and the saved-refinement backward
+    (streaming kernel, delta from the saved output), on grids where a group
+    takes several tokens in turn: the forward output is the same bits, dv
+    agrees to BF16 rounding and dq to the refinement's delta error."""
+    producer, query, upstream = _inputs(sources, tokens, width, rank, False, SEEDS[1] + width + tokens)
+    values = producer.detach()
+    q = query.detach()
+    print(f"key-resident vs saved S={sources} N={tokens} D={width} R={rank} layout={layout}", flush=True)
+    results = {}
+    for save in (False, True):
+        if layout == "packed":
+            out, refine, logit, inv_rms, stats = _ops.packed_forward_impl(values, q, 2**-23, 1.0, save)
+            dv, dq = _ops.packed_backward(values, q, out, refine, upstream, logit, inv_rms, stats, 1.0)
+        else:
+            listed = list(values.unbind(0))
+            out, refine, logit, inv_rms, stats = _ops.sources_forward_impl(listed, q, 2**-23, 1.0, save)
+            grads = _ops.sources_backward(listed, q, out, refine, upstream, logit, inv_rms, stats, 1.0)
+            dv, dq = torch.stack(grads[:-1]), grads[-1]
+        assert refine.shape[0] == (tokens if save else 0)
+        results[save] = (out, dv, dq)
+    torch.cuda.synchronize()
+    (out_k, dv_k, dq_k), (out_s, dv_s, dq_s) = results[False], results[True]
+    assert torch.equal(out_k, out_s)
+    # the non-key coordinates are p dO in both kernels: the same bits (up to the sign of zero)
+    key0 = width - rank
+    assert torch.equal(dv_k[..., :key0].float(), dv_s[..., :key0].float())
+    scale_dv = float(dv_s.float().abs().max())
+    torch.testing.assert_close(dv_k.float(), dv_s.float(), rtol=2.0**-7, atol=2.0**-9 * scale_dv)
+    rel = float((dq_k.float() - dq_s.float()).norm() / dq_s.float().norm())
+    assert rel < 2e-3, rel
+
+
+@pytest.mark.parametrize("sources", [16, 17])
+def test_key_resident_policy_boundary(sources):
+    """16 sources of (4096, 1024) take the key-resident backward and save no
+    refinement; 17 save it and take the streaming kernel.  Both match the
+    oracle (17 with the saved path's delta allowance)."""
+    width, rank, tokens = 4096, 1024, 67
+    producer, query, upstream = _inputs(sources, tokens, width, rank, False, SEEDS[2] + sources)
+    values = producer.detach()
+    out, refine, *_ = _ops.packed_forward_impl(values, query.detach(), 2**-23, 1.0,
+                                               _ops.saves_refinement(sources, width, rank))
+    assert refine.shape[0] == (0 if sources == 16 else tokens)
+
+    def make(leaves, q):
+        return leaves[0], q
+
+    set_case(f"key-resident boundary S={sources}")
+    actual = attnres(producer, query)
+    grads = torch.autograd.grad(actual, (producer, query), upstream)
+    expected, exact = both_oracles(make, [producer], query, upstream)
+    compare_read((actual, *grads), expected, exact, ["out", "dv", "dq"], sources=sources)

@@ -154,15 +154,29 @@ def test_accumulating_backward_needs_its_flags_and_checks_like_the_plain_one():
 def test_save_recompute_policy_matches_the_header_and_the_ops():
     """Reads of at most ATTNRES_RECOMPUTE_MAX_SOURCES sources save no
     refinement (the reference recomputes for S <= 3, fla_full_sources.py:146-161;
-    the register-resident backward pays up to 6 here)."""
+    the register-resident backward pays up to 6 here), and neither do reads of
+    at most ATTNRES_KEYRES_MAX_SOURCES whose key is the last 512 or 1024
+    elements of a 2048- or 4096-wide row (the key-resident backward).  The
+    library and the ops agree on every shape class."""
     from attnres import _ops
 
     lib = _native.load()
     text = HEADER.read_text()
     assert f"#define ATTNRES_RECOMPUTE_MAX_SOURCES {_ops.RECOMPUTE_MAX_SOURCES}" in text
-    assert _ops.RECOMPUTE_MAX_SOURCES == 6
+    assert f"#define ATTNRES_KEYRES_MAX_SOURCES {_ops.KEYRES_MAX_SOURCES}" in text
+    assert _ops.RECOMPUTE_MAX_SOURCES == 6 and _ops.KEYRES_MAX_SOURCES == 16
     for count in range(1, 130):
-        assert bool(lib.attnres_hip_saves_refinement(count)) == _ops.saves_refinement(count) == (count > 6)
+        assert bool(lib.attnres_hip_saves_refinement(count)) == (count > 6)
+    key_resident = {(2048, 512), (2048, 1024), (4096, 512), (4096, 1024)}
+    widths = (1, 8, 64, 100, 512, 1000, 1024, 1536, 2040, 2048, 2056, 3072, 4096, 5000, 8192)
+    for width in widths:
+        for rank in sorted({1, 8, 256, 511, 512, 513, 768, 1024, 1536, 2048, 3072, width // 2, width} - {0}):
+            if rank > width:
+                continue
+            for count in (1, 6, 7, 9, 16, 17, 25, 129):
+                expected = count > 6 and not (count <= 16 and (width, rank) in key_resident)
+                assert _ops.saves_refinement(count, width, rank) == expected, (count, width, rank)
+                assert bool(lib.attnres_hip_saves_refinement_for(count, width, rank)) == expected, (count, width, rank)
 
 
 def test_backward_without_the_refinement_is_for_small_reads_only():
@@ -176,6 +190,15 @@ def test_backward_without_the_refinement_is_for_small_reads_only():
         _FAKE, 64, 64, 7, 4, 64, _FAKE, 16, 1.0, None, None, _FAKE, *stats, _FAKE, _FAKE, _FAKE, need, None)
     assert status == _native.ERR_SHAPE
     assert b"n_sources <= 6" in lib.attnres_hip_last_error()
+    # the key-resident backward: 16 sources of 4096-wide rows with a 1024 key pass
+    # the checks up to the workspace; 17 sources, or a key of 768, do not
+    need_wide = lib.attnres_hip_dq_workspace_elems(4, 4096, 1024)
+    for count, rank, expected in ((16, 1024, _native.ERR_WORKSPACE), (17, 1024, _native.ERR_SHAPE),
+                                  (16, 768, _native.ERR_SHAPE)):
+        status = lib.attnres_hip_packed_backward(
+            _FAKE, 4096 * 4, 4096, count, 4, 4096, _FAKE, rank, 1.0, None, None, _FAKE, *stats, _FAKE, _FAKE, _FAKE,
+            lib.attnres_hip_dq_workspace_elems(4, 4096, rank) - 1 if rank == 1024 else need_wide, None)
+        assert status == expected, (count, rank)
     status = lib.attnres_hip_packed_backward(  # small read: checks pass up to the workspace
         _FAKE, 64, 64, 6, 4, 64, _FAKE, 16, 1.0, None, None, _FAKE, *stats, _FAKE, _FAKE, _FAKE, need - 1, None)
     assert status == _native.ERR_WORKSPACE
@@ -307,3 +330,23 @@ def test_no_alloc_backward_checks_arguments_on_the_host():
     args[7] = 64
     assert lib.attnres_hip_packed_backward_noalloc(*args) == _native.ERR_NULL_POINTER
     assert b"attnres_hip_packed_backward_noalloc" in lib.attnres_hip_last_error()
+
+
+def test_no_alloc_backward_runs_every_check_before_touching_the_device():
+    """The recompute, stride and scale checks of the no-allocation backward
+    name that entry point and run before it looks up its device scratch, so
+    they return their own codes on a machine without a GPU (a device lookup
+    would fail with ATTNRES_ERR_LAUNCH instead)."""
+    lib = _native.load()
+    fake = ctypes.c_void_p(16)
+    # S = 7 without out_refine: the recompute kernel takes at most 6 sources
+    args = [fake, 0, 64, 7, 4, 64, fake, 64, 1.0, None, None, fake, fake, fake, fake, fake, fake, None]
+    assert lib.attnres_hip_packed_backward_noalloc(*args) == _native.ERR_SHAPE
+    assert b"attnres_hip_packed_backward_noalloc" in lib.attnres_hip_last_error()
+    args[3] = 2  # a small read may recompute; now a negative row stride
+    args[2] = -64
+    assert lib.attnres_hip_packed_backward_noalloc(*args) == _native.ERR_STRIDE
+    assert b"attnres_hip_packed_backward_noalloc" in lib.attnres_hip_last_error()
+    args[2] = 64
+    args[8] = float("nan")
+    assert lib.attnres_hip_packed_backward_noalloc(*args) == _native.ERR_SCALAR

@@ -172,3 +172,70 @@ def test_dropped_refinement_fails_the_query_gradient_bound(case):
 def test_floor_lies_below_a_bf16_ulp_of_the_row():
     # half a BF16 ulp of the row maximum is at least 2^-9 of it
     assert FLOOR == 2.0**-16 and math.log2(FLOOR) < -9
+
+
+# ------------------------------------------------- gradients summed over reads
+
+def _read_grads(values, query, grad_out, scale, delta_from="refined", key_factor=1.0, eps=2**-23):
+    """One read's float64 dv with delta from the refined BF16 output
+    ("refined", the saving kernels) or exact ("exact"); the key-coordinate
+    term scaled by ``key_factor`` (a planted mistake when not 1)."""
+    v = values.double()
+    q = query.double()
+    g = grad_out.double()
+    width, rank = v.shape[-1], q.numel()
+    key = v[..., width - rank:]
+    inv_rms = torch.rsqrt(key.square().mean(-1) + eps)
+    logit = (key * inv_rms[..., None] * q).sum(-1) * scale
+    weight = logit.softmax(0)
+    out = (weight[..., None] * v).sum(0)
+    if delta_from == "refined":
+        rounded = out.float().to(torch.bfloat16).double()
+        unit = bf16_ulp(rounded) / 256
+        out = rounded + torch.clamp(torch.round((out - rounded) / unit), -127, 127) * unit
+    dz = weight * ((v * g).sum(-1) - (g * out).sum(-1))
+    dv = weight[..., None] * g
+    dv[..., width - rank:] += key_factor * dz[..., None] * (
+        scale * inv_rms[..., None] * q - (inv_rms * inv_rms * logit / rank)[..., None] * key)
+    return dv
+
+
+def _bf16_running_sum(contributions):
+    """The accumulating BF16 backward: the first read writes bf16(dv), each
+    later one bf16(old + dv) with the addition in FP32."""
+    total = None
+    for dv in contributions:
+        step = dv.float() if total is None else total.float() + dv.float()
+        total = step.to(torch.bfloat16)
+    return total
+
+
+def _shared_reads(width, rank, seed):
+    generator = torch.Generator().manual_seed(seed)
+    values = torch.stack([(torch.randn(64, width, generator=generator) * (0.5 + s / 4)).to(torch.bfloat16)
+                          for s in range(9)])
+    reads = [((torch.randn(rank, generator=generator) / math.sqrt(rank)).to(torch.bfloat16),
+              torch.randn(64, width, generator=generator).to(torch.bfloat16), scale) for scale in (1.0, 0.5, 2.0)]
+    return values, reads
+
+
+@pytest.mark.parametrize("width,rank", [(2048, 2048), (1000, 96)])
+def test_accumulated_bound_holds_and_catches_a_key_term_mistake(width, rank):
+    """Three reads of nine shared sources (`SharedSources`, c4-like): the
+    emulated accumulating backward stays within `helpers.accumulated_bound`
+    of the exact sum over the reads, and a 1% error in one read's key term
+    (the routing gradient on the key coordinates) exceeds it."""
+    from helpers import accumulated_bound
+
+    values, reads = _shared_reads(width, rank, seed=20261202 + width)
+    exact = [_read_grads(values, q, g, s, "exact") for q, g, s in reads]
+    allowances = [delta_allowance(values.double(), q.double(), g.double(), scale=s)[0] for q, g, s in reads]
+    bound = accumulated_bound(exact, allowances, roundings=len(reads))
+    total = sum(exact)
+    emulated = _bf16_running_sum([_read_grads(values, q, g, s) for q, g, s in reads])
+    ratio = float(((emulated.double() - total).abs() / bound).max())
+    assert ratio <= 1.0, ratio
+    mistaken = _bf16_running_sum([_read_grads(values, q, g, s, key_factor=1.01 if i == 1 else 1.0)
+                                  for i, (q, g, s) in enumerate(reads)])
+    planted = float(((mistaken.double() - total).abs() / bound).max())
+    assert planted > 2.0, planted
