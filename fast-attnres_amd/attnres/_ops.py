@@ -33,9 +33,10 @@ refinement byte per element (together the FP32 mix to ulp/512, for
 ``delta = <dO, o>``).  Smaller reads save neither: ``out_refine`` is
 ``[0, D]`` and their backward derives delta from the value rows it reads
 anyway; so do reads of up to ``KEYRES_MAX_SOURCES`` sources whose key is the
-last 512 or 1024 elements of a 2048- or 4096-wide row (`keyres_key_chunks`:
-the key-resident backward holds the key coordinates of a token's rows until
-delta is complete).  The reference makes the same structural choice
+last 512 or 1024 elements of a 2048- or 4096-wide row, and of up to
+``KEYRES_FULL_MAX_SOURCES`` with the whole 2048-wide row as key
+(`keyres_key_chunks`: the key-resident backward holds the key coordinates of a
+token's rows until delta is complete).  The reference makes the same structural choice
 (`fla_full_sources._should_save_mixed`, `fla_full_sources.py:146-161`:
 recompute for S <= 3) but saves an FP32 copy of the output for larger reads
 (`fixed_tail.py:917-919`): four extra bytes per element written in the
@@ -62,7 +63,8 @@ _BF16 = torch.bfloat16
 # Save/recompute policy (attnres_hip.h ATTNRES_RECOMPUTE_MAX_SOURCES,
 # ATTNRES_KEYRES_MAX_SOURCES; attnres_hip_saves_refinement_for).
 RECOMPUTE_MAX_SOURCES = 6
-KEYRES_MAX_SOURCES = 16
+KEYRES_MAX_SOURCES = 16       # key of 512 or 1024 of a 2048- or 4096-wide row
+KEYRES_FULL_MAX_SOURCES = 12  # the whole 2048-wide row as key
 _KEY_COLUMN = 512  # elements per chunk column of a 64-lane row (64 lanes x 8)
 
 
@@ -70,26 +72,31 @@ def keyres_key_chunks(width: int, rank: int) -> int:
     """Chunk columns of the key when the key-resident backward applies to a
     read of this width and rank: rows of 2048 or 4096 elements (64-lane
     groups, every chunk in range) whose key is their last 512 or 1024
-    elements; 0 otherwise."""
+    elements (1 or 2 columns), or whole rows of 2048 (4 columns); 0 otherwise."""
     if not 1024 < width <= 4096:
         return 0
     chunks = 4 if width <= 2048 else 8
-    if width != chunks * _KEY_COLUMN or rank >= width or rank % _KEY_COLUMN:
+    if width != chunks * _KEY_COLUMN or rank % _KEY_COLUMN:
         return 0
     key_chunks = rank // _KEY_COLUMN
+    if key_chunks == chunks:
+        return key_chunks if chunks == 4 else 0
     return key_chunks if key_chunks <= 2 else 0
 
 
 def saves_refinement(sources: int, width: int, rank: int) -> bool:
     """Whether a read saves its output refinement for the backward (else the
     backward takes delta from the value rows: every read of at most
-    ``RECOMPUTE_MAX_SOURCES`` sources, and reads of at most
-    ``KEYRES_MAX_SOURCES`` whose key the key-resident backward holds).
-    Reference `fla_full_sources._should_save_mixed`, `fla_full_sources.py:146-161`,
-    keys on the source count alone."""
+    ``RECOMPUTE_MAX_SOURCES`` sources, and reads whose key the key-resident
+    backward holds, up to ``KEYRES_MAX_SOURCES`` sources for a partial key and
+    ``KEYRES_FULL_MAX_SOURCES`` for the whole row).  Reference
+    `fla_full_sources._should_save_mixed`, `fla_full_sources.py:146-161`, keys
+    on the source count alone."""
     if sources <= RECOMPUTE_MAX_SOURCES:
         return False
-    return not (sources <= KEYRES_MAX_SOURCES and keyres_key_chunks(width, rank) > 0)
+    key_chunks = keyres_key_chunks(width, rank)
+    limit = KEYRES_FULL_MAX_SOURCES if key_chunks == 4 else KEYRES_MAX_SOURCES
+    return not (key_chunks > 0 and sources <= limit)
 
 
 def _refine_rows(sources: int, tokens: int, width: int, rank: int) -> int:
@@ -176,18 +183,26 @@ def _dq_workspace(lib, n_tokens: int, width: int, rank: int, device) -> Tensor:
     return torch.empty((elems,), device=device, dtype=_F32)
 
 
-def _statistics(tokens: int, sources: int, device, pooled: bool) -> tuple[Tensor, Tensor, Tensor]:
-    """logit ``[N, S]``, inv_rms ``[N, S]`` and stats ``[2, N]`` (FP32).
-    ``pooled``: views of one allocation, for callers that keep them together
-    (not for custom-op outputs, which must not alias each other)."""
+def _saved_state(tokens: int, sources: int, width: int, save: bool, device,
+                 pooled: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """out_refine ``[N, D]`` int8 (``[0, D]`` when not saved), logit ``[N, S]``,
+    inv_rms ``[N, S]`` and stats ``[2, N]`` (FP32).  ``pooled``: views of one
+    byte allocation, for callers that keep them together (not for custom-op
+    outputs, which must not alias each other); a small read then pays one
+    allocation here instead of four."""
+    refine_rows = tokens if save else 0
     if not pooled:
-        return (torch.empty((tokens, sources), device=device, dtype=_F32),
+        return (torch.empty((refine_rows, width), device=device, dtype=torch.int8),
+                torch.empty((tokens, sources), device=device, dtype=_F32),
                 torch.empty((tokens, sources), device=device, dtype=_F32),
                 torch.empty((2, tokens), device=device, dtype=_F32))
     block = tokens * sources
-    pool = torch.empty((2 * block + 2 * tokens,), device=device, dtype=_F32)
-    return (pool[:block].view(tokens, sources), pool[block:2 * block].view(tokens, sources),
-            pool[2 * block:].view(2, tokens))
+    head = (refine_rows * width + 15) // 16 * 16  # the FP32 part starts 16-byte aligned
+    pool = torch.empty((head + 4 * (2 * block + 2 * tokens),), device=device, dtype=torch.uint8)
+    floats = pool[head:].view(_F32)
+    return (pool[:refine_rows * width].view(torch.int8).view(refine_rows, width),
+            floats[:block].view(tokens, sources), floats[block:2 * block].view(tokens, sources),
+            floats[2 * block:].view(2, tokens))
 
 
 # ------------------------------------------------------------------ packed
@@ -196,15 +211,14 @@ def packed_forward_impl(values: Tensor, query: Tensor, eps: float, scale: float,
                         save: bool, pooled: bool = False) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """The packed forward launch; ``save`` chooses whether the refinement is
     stored (``out_refine`` ``[N, D]``) or not (``[0, D]``); ``pooled`` as for
-    ``_statistics``."""
+    ``_saved_state``."""
     lib = _native.load()
     values = _unit_feature_stride(values)
     query = _contiguous(query)
     sources, tokens, width = (int(size) for size in values.shape)
     device = values.device
     out = torch.empty((tokens, width), device=device, dtype=_BF16)
-    out_refine = torch.empty((tokens if save else 0, width), device=device, dtype=torch.int8)
-    logit, inv_rms, stats = _statistics(tokens, sources, device, pooled)
+    out_refine, logit, inv_rms, stats = _saved_state(tokens, sources, width, save, device, pooled)
     with _on_device(device):
         status = lib.attnres_hip_packed_forward(
             values.data_ptr(), values.stride(0), values.stride(1), sources, tokens, width,
@@ -314,7 +328,8 @@ class _PackedRead(torch.autograd.Function):
     @staticmethod
     def forward(ctx, values: Tensor, query: Tensor, eps: float, scale: float):
         outputs = packed_forward_impl(values, query, eps, scale,
-                                      saves_refinement(int(values.shape[0]), int(values.shape[-1]), query.numel()))
+                                      saves_refinement(int(values.shape[0]), int(values.shape[-1]), query.numel()),
+                                      pooled=True)
         _packed_setup_context(ctx, (values, query, eps, scale), outputs)
         return outputs
 
@@ -369,8 +384,7 @@ def sources_forward_impl(sources: list[Tensor], query: Tensor, eps: float, scale
     device = first.device
     prepared, pointers, row_strides = _source_table(sources)
     out = torch.empty(first.shape, device=device, dtype=_BF16)
-    out_refine = torch.empty((tokens if save else 0, width), device=device, dtype=torch.int8)
-    logit, inv_rms, stats = _statistics(tokens, count, device, pooled)
+    out_refine, logit, inv_rms, stats = _saved_state(tokens, count, width, save, device, pooled)
     with _on_device(device):
         status = lib.attnres_hip_sources_forward(
             pointers, row_strides, count, tokens, width, query.data_ptr(), query.numel(),
@@ -479,7 +493,8 @@ class _SourcesRead(torch.autograd.Function):
     @staticmethod
     def forward(ctx, query: Tensor, eps: float, scale: float, *sources: Tensor):
         outputs = sources_forward_impl(list(sources), query, eps, scale,
-                                       saves_refinement(len(sources), int(sources[0].shape[-1]), query.numel()))
+                                       saves_refinement(len(sources), int(sources[0].shape[-1]), query.numel()),
+                                       pooled=True)
         _sources_setup_context(ctx, (sources, query, eps, scale), outputs)
         return outputs
 
@@ -506,7 +521,7 @@ def sources_attnres(sources: tuple[Tensor, ...], query: Tensor, eps: float,
 
 
 __all__ = [
-    "KEYRES_MAX_SOURCES", "RECOMPUTE_MAX_SOURCES", "keyres_key_chunks", "packed_attnres", "packed_backward", "packed_backward_impl", "packed_forward",
+    "KEYRES_FULL_MAX_SOURCES", "KEYRES_MAX_SOURCES", "RECOMPUTE_MAX_SOURCES", "keyres_key_chunks", "packed_attnres", "packed_backward", "packed_backward_impl", "packed_forward",
     "packed_forward_impl", "prepare_rows", "row_stride", "saves_refinement", "sources_attnres", "sources_backward",
     "sources_backward_impl", "sources_forward", "sources_forward_impl",
 ]

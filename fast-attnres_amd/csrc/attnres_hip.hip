@@ -332,8 +332,10 @@ int check_recompute(bool recompute, int64_t S, int64_t D, int64_t R, const char*
   if (recompute && !recomputes(S, D, R))
     return fail(ATTNRES_ERR_SHAPE,
                 "%s without out_refine needs n_sources <= %d, or <= %d with a key of 512 or 1024 whole "
-                "columns of a 2048- or 4096-wide row (got n_sources=%lld, width=%lld, rank=%lld)",
-                name, kRecomputeMaxSources, kKeyResMaxSources, (long long)S, (long long)D, (long long)R);
+                "columns of a 2048- or 4096-wide row, or <= %d with width = rank = 2048 (got n_sources=%lld, "
+                "width=%lld, rank=%lld)",
+                name, kRecomputeMaxSources, kKeyResMaxSources, kKeyResFullMaxSources, (long long)S, (long long)D,
+                (long long)R);
   return ATTNRES_OK;
 }
 

@@ -197,26 +197,35 @@ inline bool no_mask(const Geometry& geo, int64_t width, int64_t rank) {
 }
 
 // Key-resident backward (attnres_bwd_keyres_kernel): reads of more than
-// kRecomputeMaxSources and at most kKeyResMaxSources sources whose rows are
-// full 64-lane geometry rows (D = 64 * CH * 8) and whose key is the last
-// KC <= kKeyResMaxChunks whole chunk columns (R = KC * 512, R < D) save no
-// refinement either: the backward keeps the key chunks of a token's rows in
-// registers and takes delta from the value rows.  Returns KC, or 0 where the
-// kernel does not apply.
+// kRecomputeMaxSources sources whose rows are full 64-lane geometry rows
+// (D = 64 * CH * 8) and whose key is the last KC whole chunk columns
+// (R = KC * 512) save no refinement either: the backward keeps the key chunks
+// of a token's rows in registers and takes delta from the value rows.  A key
+// of 1 or 2 columns (R = 512 or 1024 < D) is held for up to
+// kKeyResMaxSources sources; a full row of 4 columns (D = R = 2048) for up to
+// kKeyResFullMaxSources.  Returns KC, or 0 where the kernel does not apply.
 constexpr int kKeyResMaxSources = ATTNRES_KEYRES_MAX_SOURCES;
+constexpr int kKeyResFullMaxSources = ATTNRES_KEYRES_FULL_MAX_SOURCES;
 constexpr int kKeyResMaxChunks = 2;
+constexpr int kKeyResFullChunks = 4;
 inline int keyres_key_chunks(int64_t D, int64_t R) {
   const Geometry geo = geometry(D);
   const int64_t column = static_cast<int64_t>(geo.lanes) * kVec;  // elements per chunk column
-  if (geo.lanes != 64 || D != geo.chunks * column || R >= D || R % column != 0) return 0;
+  if (geo.lanes != 64 || D != geo.chunks * column || R % column != 0) return 0;
   const int64_t kc = R / column;
+  if (kc == geo.chunks) return kc == kKeyResFullChunks ? static_cast<int>(kc) : 0;  // R = D = 2048 only
   return kc <= kKeyResMaxChunks ? static_cast<int>(kc) : 0;
 }
+
+// The most sources the key-resident backward holds for a key of kc columns.
+constexpr int keyres_max_sources(int kc) { return kc == kKeyResFullChunks ? kKeyResFullMaxSources : kKeyResMaxSources; }
 
 // Whether a read of S sources, width D and rank R can run its backward
 // without the saved output and refinement (the save/recompute policy).
 inline bool recomputes(int64_t S, int64_t D, int64_t R) {
-  return S <= kRecomputeMaxSources || (S <= kKeyResMaxSources && keyres_key_chunks(D, R) > 0);
+  if (S <= kRecomputeMaxSources) return true;
+  const int kc = keyres_key_chunks(D, R);
+  return kc > 0 && S <= keyres_max_sources(kc);
 }
 
 // Lanes per token group of the recompute backward: it keeps S rows per lane,

@@ -44,9 +44,10 @@
 // holds all S rows of its token and takes delta = sum_s p_s dw_s from them,
 // so the forward stores no refinement and the backward reads no saved output
 // (attnres_bwd_recompute_kernel).  Reads of up to 16 sources whose key is a
-// suffix of whole chunk columns (R = 512 or 1024 of D = 2048 or 4096) do the
-// same while streaming their rows: only the key chunks of a token's rows are
-// held until delta is complete (attnres_bwd_keyres_kernel).  The accumulating variant adds dv to
+// suffix of whole chunk columns (R = 512 or 1024 of D = 2048 or 4096), and of
+// up to 12 with D = R = 2048, do the same while streaming their rows: only the
+// key chunks of a token's rows are held until delta is complete
+// (attnres_bwd_keyres_kernel).  The accumulating variant adds dv to
 // existing gradient rows (BF16, or FP32 sums for a source bank).  The
 // coefficient variant writes no dv at all, only the per-token terms p, a, b;
 // a source bank later forms each source's gradient once from the dO rows of
@@ -1399,8 +1400,9 @@ __global__ void __launch_bounds__(kBlock) attnres_bwd_recompute_kernel(const Bwd
 
 // ------------------------------------------- backward, key-resident (R < D)
 
-// For a read whose key is a proper suffix of whole chunk columns (D = G*CH*8,
-// R = KC*G*8, KC < CH) of at most KS sources, the forward stores no
+// For a read whose key is a suffix of whole chunk columns (D = G*CH*8,
+// R = KC*G*8: KC = 1 or 2 of 4 or 8 columns, or the whole row of 4 columns,
+// D = R = 2048) of at most KS sources, the forward stores no
 // refinement and this backward reads neither the output nor its refinement,
 // like the recompute kernel, but it streams the value rows through a ring
 // instead of holding whole tokens.  Only the key coordinates of dv depend on
@@ -1426,7 +1428,7 @@ template <int G, int CH, int KC, int KS, int NB, bool LAG, bool VEC, class Rows,
 __global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, 1)))
 attnres_bwd_keyres_kernel(const BwdArgs<Rows, Grads> a) {
   static_assert(G == 64, "one wavefront per token group");
-  static_assert(KC >= 1 && KC < CH, "the key is a proper suffix of whole chunk columns");
+  static_assert(KC >= 1 && KC <= CH, "the key is a suffix of whole chunk columns");
   static_assert(KS % NB == 0, "whole ring rounds per token");
   static_assert(std::is_same_v<Grads, PackedGrads> || std::is_same_v<Grads, ListGrads>, "BF16 dv rows");
   constexpr int C0 = CH - KC;  // first key chunk column
@@ -2073,14 +2075,21 @@ int64_t launch_bwd_recompute(const BwdArgs<Rows, Grads>& a, hipStream_t stream) 
 // (c3: 390 -> 372 us); the backward moves 4% fewer bytes at about the same
 // time.  A first version that formed every key part at the token's end (two
 // rows in flight over that burst) took 862 us for the c3 backward.
+//
+// The whole 2048-wide row as key (KC = CH = 4, up to 12 sources, 192 VGPRs of
+// held rows; 256 VGPRs + 202 AGPRs aligned) streams the rows the recompute
+// kernel holds all at once.  Measured on MI355X (fwd + bwd per read, us, saved
+// refinement -> key-resident, D = R = 2048): S = 9, N = 32768 (c4's shape):
+// 722.1 -> 698.7; S = 7: 299.7 -> 291.6; S = 12: 459.0 -> 446.7; S = 9,
+// N = 16384: 358.6 -> 352.4.
 template <int G, int CH, int KC, bool VEC, class Rows, class Grads>
 int64_t launch_bwd_keyres_chunks(const BwdArgs<Rows, Grads>& a, hipStream_t stream) {
   constexpr int NB = 2;
   constexpr bool LAG = CH == 8;
-  const int64_t resident =
-      resident_blocks<&attnres_bwd_keyres_kernel<G, CH, KC, kKeyResMaxSources, NB, LAG, VEC, Rows, Grads>>();
+  constexpr int KS = keyres_max_sources(KC);
+  const int64_t resident = resident_blocks<&attnres_bwd_keyres_kernel<G, CH, KC, KS, NB, LAG, VEC, Rows, Grads>>();
   const int64_t blocks = grid_blocks(a.n_tokens, G, kBwdGridPerResident * resident, a.max_grid);
-  hipLaunchKernelGGL((attnres_bwd_keyres_kernel<G, CH, KC, kKeyResMaxSources, NB, LAG, VEC, Rows, Grads>),
+  hipLaunchKernelGGL((attnres_bwd_keyres_kernel<G, CH, KC, KS, NB, LAG, VEC, Rows, Grads>),
                      dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream, a);
   return blocks;
 }
@@ -2093,6 +2102,12 @@ int64_t launch_bwd_keyres(const BwdArgs<Rows, Grads>& a, bool vec, hipStream_t s
                          : launch_bwd_keyres_chunks<G, CH, 1, false>(a, stream);
       case 2: return vec ? launch_bwd_keyres_chunks<G, CH, 2, true>(a, stream)
                          : launch_bwd_keyres_chunks<G, CH, 2, false>(a, stream);
+      case kKeyResFullChunks:
+        if constexpr (CH == kKeyResFullChunks) {
+          return vec ? launch_bwd_keyres_chunks<G, CH, CH, true>(a, stream)
+                     : launch_bwd_keyres_chunks<G, CH, CH, false>(a, stream);
+        }
+        break;
       default: break;
     }
   }

@@ -46,8 +46,10 @@
  * backward, which then derives delta = <dO, o> = sum_s p_s <v_s, dO> from
  * the value rows it reads anyway.  So need reads of at most
  * ATTNRES_KEYRES_MAX_SOURCES whose rows are 2048 or 4096 elements wide and
- * whose key is their last 512 or 1024 (the key-resident backward keeps the
- * key coordinates of a token's rows in registers while the rows stream by).
+ * whose key is their last 512 or 1024, and reads of at most
+ * ATTNRES_KEYRES_FULL_MAX_SOURCES of 2048-wide rows with R = D (the
+ * key-resident backward keeps the key coordinates of a token's rows in
+ * registers while the rows stream by).
  * attnres_hip_saves_refinement_for tells them apart; other reads must save
  * it.  (The reference makes the same structural choice with a threshold of
  * 3: recompute for S <= 3, save the FP32 mixed output for S >= 4,
@@ -78,9 +80,12 @@ enum attnres_status {
 #define ATTNRES_MAX_WIDTH 8192
 /* Reads of at most this many sources may skip the refinement (see above). */
 #define ATTNRES_RECOMPUTE_MAX_SOURCES 6
-/* The key-resident backward takes reads of up to this many sources (see
+/* The key-resident backward takes reads of up to this many sources with a
+ * key of 512 or 1024 of 2048- or 4096-wide rows, and of up to
+ * ATTNRES_KEYRES_FULL_MAX_SOURCES with the whole 2048-wide row as key (see
  * attnres_hip_saves_refinement_for). */
 #define ATTNRES_KEYRES_MAX_SOURCES 16
+#define ATTNRES_KEYRES_FULL_MAX_SOURCES 12
 
 /* Element types of attnres_hip_partial_sum and attnres_hip_bank_gather. */
 #define ATTNRES_DTYPE_F32 0
@@ -108,9 +113,10 @@ int attnres_hip_saves_refinement(int64_t n_sources);
  * The save/recompute policy for a read of the given shape: 0 (recompute) for
  * n_sources <= ATTNRES_RECOMPUTE_MAX_SOURCES, and also for
  * n_sources <= ATTNRES_KEYRES_MAX_SOURCES when the rows are 2048 or 4096
- * elements wide and the key is their last 512 or 1024 (the key-resident
- * backward: it holds the key coordinates of a token's rows and takes delta
- * from the value rows); 1 (save) otherwise.  The forward of a recomputing
+ * elements wide and the key is their last 512 or 1024, and for
+ * n_sources <= ATTNRES_KEYRES_FULL_MAX_SOURCES when width = rank = 2048 (the
+ * key-resident backward: it holds the key coordinates of a token's rows and
+ * takes delta from the value rows); 1 (save) otherwise.  The forward of a recomputing
  * read may pass out_refine = NULL, and its backward must then get
  * out = out_refine = NULL.  Host-only.  Replaces `_should_save_mixed`
  * (fla_full_sources.py:146-161), which keys on the source count alone.

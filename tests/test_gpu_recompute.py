@@ -122,10 +122,13 @@ def test_recompute_special_cases_are_exact():
 KEYRES_SHAPES = [(2048, 512), (2048, 1024), (4096, 512), (4096, 1024)]
 
 
+KEYRES_CASES = [(s, w, r) for s in (7, 8, 13, 16) for w, r in KEYRES_SHAPES] + \
+    [(s, 2048, 2048) for s in (7, 9, 12)]  # the whole 2048-wide row as key, up to 12 sources
+
+
 @pytest.mark.parametrize("layout", ["packed", "list"])
 @pytest.mark.parametrize("padded", [False, True], ids=["aligned", "padded"])
-@pytest.mark.parametrize("width,rank", KEYRES_SHAPES, ids=lambda v: str(v))
-@pytest.mark.parametrize("sources", [7, 8, 13, 16])
+@pytest.mark.parametrize("sources,width,rank", KEYRES_CASES, ids=lambda v: str(v))
 def test_key_resident_backward_matches_oracle(sources, width, rank, padded, layout):
     """Against the oracle at the full bars with no delta allowance: delta is
     an FP32 sum over the value rows, not the refined BF16 output.  Padded rows
@@ -149,8 +152,9 @@ def test_key_resident_backward_matches_oracle(sources, width, rank, padded, layo
 
 
 @pytest.mark.parametrize("layout", ["packed", "list"])
-@pytest.mark.parametrize("width,rank", KEYRES_SHAPES, ids=lambda v: str(v))
-@pytest.mark.parametrize("sources,tokens", [(7, 5003), (16, 2053), (9, 1)], ids=lambda v: str(v))
+@pytest.mark.parametrize("sources,tokens,width,rank",
+                         [(s, n, w, r) for s, n in ((7, 5003), (16, 2053), (9, 1)) for w, r in KEYRES_SHAPES] +
+                         [(7, 5003, 2048, 2048), (12, 2053, 2048, 2048), (9, 1, 2048, 2048)], ids=lambda v: str(v))
 def test_key_resident_agrees_with_the_saved_refinement_path(sources, tokens, width, rank, layout):
     """Same inputs through the key-resident and the saved-refinement backward
     (streaming kernel, delta from the saved output), on grids where a group
@@ -184,17 +188,19 @@ def test_key_resident_agrees_with_the_saved_refinement_path(sources, tokens, wid
     assert rel < 2e-3, rel
 
 
-@pytest.mark.parametrize("sources", [16, 17])
-def test_key_resident_policy_boundary(sources):
-    """16 sources of (4096, 1024) take the key-resident backward and save no
-    refinement; 17 save it and take the streaming kernel.  Both match the
-    oracle (17 with the saved path's delta allowance)."""
-    width, rank, tokens = 4096, 1024, 67
+@pytest.mark.parametrize("sources,width,rank", [(16, 4096, 1024), (17, 4096, 1024), (12, 2048, 2048),
+                                                (13, 2048, 2048)], ids=lambda v: str(v))
+def test_key_resident_policy_boundary(sources, width, rank):
+    """16 sources of (4096, 1024) and 12 of (2048, 2048) take the key-resident
+    backward and save no refinement; 17 and 13 save it (the streaming and the
+    token-block backward).  All match the oracle (the saving reads with the
+    saved path's delta allowance)."""
+    tokens = 67
     producer, query, upstream = _inputs(sources, tokens, width, rank, False, SEEDS[2] + sources)
     values = producer.detach()
     out, refine, *_ = _ops.packed_forward_impl(values, query.detach(), 2**-23, 1.0,
                                                _ops.saves_refinement(sources, width, rank))
-    assert refine.shape[0] == (0 if sources == 16 else tokens)
+    assert refine.shape[0] == (0 if sources in (12, 16) else tokens)
 
     def make(leaves, q):
         return leaves[0], q

@@ -19,7 +19,7 @@ import pytest
 import torch
 
 from attnres import SharedSources, attnres
-from helpers import compare, ulp_error
+from helpers import accumulated_bound, check_accumulated, compare, exact_grads, oracle_grads, set_case, ulp_error
 from oracle.oracle import oracle
 
 pytestmark = pytest.mark.gpu
@@ -58,16 +58,29 @@ def test_shared_sources_match_autograd_sums_and_the_oracle(width, rank):
         # dq: the same terms summed in the order of each kernel's grid; at D = 2048, R = D the
         # plain read runs the token-block backward, whose grid differs from the accumulating one
         assert ulp_error(a, b.double()) <= 1.0
-    for a, b in zip(grads_bank[:count], grads_ref[:count]):
-        # two BF16 roundings of partial sums apart at most, on the scale of the gradient
-        torch.testing.assert_close(a.float(), b.float(), rtol=2.0**-6, atol=2.0**-6 * float(b.float().abs().max()))
-    cpu_src = [t.detach().cpu().requires_grad_() for t in src]
-    cpu_q = [q.detach().cpu().requires_grad_() for q in queries]
-    outs_cpu = [oracle(tuple(cpu_src), q, scale=s) for q, s in zip(cpu_q, scales)]
-    loss = sum((o.float() * g.cpu().float()).sum() for o, g in zip(outs_cpu, grads))
-    grads_cpu = torch.autograd.grad(loss, (*cpu_src, *cpu_q))
-    for a, e in zip(grads_bank, grads_cpu):
-        compare(a, e)
+    _check_against_float64(src, queries, grads, scales, grads_bank, f"shared sources D={width} R={rank}")
+
+
+def _check_against_float64(src, queries, grads, scales, results, case):
+    """Each source's gradient summed over the reads by the accumulating
+    kernel against the exact sum of the reads' float64 gradients, within
+    `helpers.accumulated_bound`: one BF16 rounding per read (the first read
+    writes bf16(dv), each later one bf16(old + dv)), each read's FP32 floor
+    and its delta allowance (these reads save their output).  Each query's
+    gradient is one read's dq: one ulp of float64 plus its allowance, and the
+    BF16 oracle's gate."""
+    count = len(src)
+    make = lambda leaves, q: (tuple(leaves), q)  # noqa: E731
+    per_read = [exact_grads(make, src, q, g, scale=s)[1] for q, g, s in zip(queries, grads, scales)]
+    set_case(case)
+    for i in range(count):
+        contributions = [grads64[i] for grads64 in per_read]
+        bound = accumulated_bound(contributions, [c.dv_allowance for c in contributions], roundings=len(per_read))
+        check_accumulated(results[i], sum(contributions), bound, f"dv{i}")
+    for r, (q, g, s) in enumerate(zip(queries, grads, scales)):
+        expected = oracle_grads(make, src, q, g, scale=s)[1][count]
+        exact = per_read[r][count]
+        compare(results[count + r], expected, exact=exact, name=f"dq{r}", extra=exact.dq_allowance)
 
 
 def test_each_backward_pass_starts_a_fresh_sum():
@@ -423,3 +436,99 @@ def test_source_bank_on_a_large_grid_matches_the_plain_stream(gradients):
     g_ref = torch.autograd.grad(outs_ref, params, grads)
     for a, b in zip(g_bank, g_ref):
         torch.testing.assert_close(a, b, rtol=2.0**-6, atol=2.0**-6 * float(b.abs().max()))
+
+
+@pytest.mark.parametrize("gradients", ["gather", "accumulate"])
+@pytest.mark.parametrize("width,rank", [(1024, 1024), (1000, 96), (2048, 512)], ids=["d1024", "d1000_r96", "d2048_r512"])
+def test_source_bank_slot_gradients_within_float64_bound(width, rank, gradients):
+    """FP32 sources pushed into a bank and read as growing prefixes (2, 3, 4,
+    5 slots): each source's gradient is an FP32 sum over the reads that saw
+    it (gathered once from the reads' dO rows and coefficients, or added read
+    by read), so against the exact float64 sum it may differ only by each
+    read's FP32 floor and delta allowance (bank reads save their output); no
+    BF16 rounding enters.  Each query's gradient is one read's dq."""
+    from attnres import SourceBank
+
+    torch.manual_seed(71 + width)
+    tokens = (2, 37)
+    leaves = [(torch.randn(*tokens, width, device="cuda") * (0.5 + s / 3)).requires_grad_() for s in range(5)]
+    counts = (2, 3, 4, 5)
+    queries = [(torch.randn(rank, device="cuda") / math.sqrt(rank)).to(torch.bfloat16).requires_grad_()
+               for _ in counts]
+    upstream = [torch.randn(*tokens, width, device="cuda") for _ in counts]
+    print(f"source bank float64 bound D={width} R={rank} gradients={gradients}", flush=True)
+    bank = SourceBank(len(leaves), gradients=gradients)
+    for leaf in leaves:
+        bank.push(leaf)
+    outs = [bank.read(q, count=c).float() for q, c in zip(queries, counts)]
+    results = torch.autograd.grad(sum((o * g).sum() for o, g in zip(outs, upstream)), (*leaves, *queries))
+    # the reads see the BF16 copies of the sources and the BF16 upstream gradient (the output's cast)
+    slots = [leaf.detach().to(torch.bfloat16) for leaf in leaves]
+    make = lambda ls, q: (tuple(ls), q)  # noqa: E731
+    per_read = [exact_grads(make, slots[:c], q, g.to(torch.bfloat16)) for q, g, c in zip(queries, upstream, counts)]
+    set_case(f"source bank D={width} R={rank} {gradients}")
+    for i, result in enumerate(results[:len(leaves)]):
+        contributions = [grads64[i] for c, (_, grads64) in zip(counts, per_read) if i < c]
+        bound = accumulated_bound(contributions, [x.dv_allowance for x in contributions], roundings=0)
+        check_accumulated(result, sum(contributions), bound, f"slot{i}")
+    for r, (q, g, c) in enumerate(zip(queries, upstream, counts)):
+        exact = per_read[r][1][c]
+        expected = oracle_grads(make, slots[:c], q, g.to(torch.bfloat16))[1][c]
+        compare(results[len(leaves) + r], expected, exact=exact, name=f"dq{r}", extra=exact.dq_allowance)
+
+
+@pytest.mark.parametrize("gradients", ["gather", "accumulate"])
+def test_source_bank_tail_reads_within_float64_bound(gradients):
+    """Block-style reads of completed slots plus a partial-sum slot (the FP32
+    source-list sums, `ListGradsF32`): blocks b0..b2 in slots 0..2, then
+    partials p1 = e0, p2 = e0 + e1, p3 = e0 + e1 + e2 (`push_sum`) read as a
+    tail slot.  Each FP32 leaf's gradient against the exact sum of the
+    contributions that reach it (a partial's gradient reaches every emitted
+    term in it), within each read's FP32 floor and delta allowance."""
+    from attnres import SourceBank
+
+    torch.manual_seed(79)
+    width, rank, tokens = 1024, 256, (2, 33)
+    blocks = [torch.randn(*tokens, width, device="cuda", requires_grad=True) for _ in range(3)]
+    emitted = [torch.randn(*tokens, width, device="cuda", requires_grad=True) for _ in range(3)]
+    queries = [(torch.randn(rank, device="cuda") / math.sqrt(rank)).to(torch.bfloat16).requires_grad_()
+               for _ in range(4)]
+    upstream = [torch.randn(*tokens, width, device="cuda") for _ in range(4)]
+    print(f"source bank tail reads float64 bound gradients={gradients}", flush=True)
+    bank = SourceBank(6, gradients=gradients)
+    for i, block in enumerate(blocks):
+        bank.push(block, slot=i)
+    bank.push(emitted[0], slot=3)
+    outs = [bank.read(queries[0], count=3, tail=3).float()]
+    partial = bank.push_sum(emitted[0], emitted[1], slot=4)
+    outs.append(bank.read(queries[1], count=3, tail=4).float())
+    bank.push_sum(partial, emitted[2], slot=5)
+    outs.append(bank.read(queries[2], count=2, tail=5).float())
+    outs.append(bank.read(queries[3], count=3).float())
+    params = (*blocks, *emitted, *queries)
+    results = torch.autograd.grad(sum((o * g).sum() for o, g in zip(outs, upstream)), params)
+
+    bf = lambda t: t.detach().to(torch.bfloat16)  # noqa: E731
+    p2 = emitted[0].detach() + emitted[1].detach()
+    p3 = p2 + emitted[2].detach()
+    # (sources of each read, which leaves each source's gradient reaches)
+    reads = [([bf(b) for b in blocks] + [bf(emitted[0])], [[0], [1], [2], [3]]),
+             ([bf(b) for b in blocks] + [bf(p2)], [[0], [1], [2], [3, 4]]),
+             ([bf(b) for b in blocks[:2]] + [bf(p3)], [[0], [1], [3, 4, 5]]),
+             ([bf(b) for b in blocks], [[0], [1], [2]])]
+    make = lambda ls, q: (tuple(ls), q)  # noqa: E731
+    contributions = [[] for _ in range(6)]
+    allowances = [[] for _ in range(6)]
+    set_case(f"source bank tail reads {gradients}")
+    for r, ((sources, reach), q, g) in enumerate(zip(reads, queries, upstream)):
+        _, grads64 = exact_grads(make, sources, q, g.to(torch.bfloat16))
+        for position, leaves_reached in enumerate(reach):
+            for leaf in leaves_reached:
+                contributions[leaf].append(grads64[position])
+                allowances[leaf].append(grads64[position].dv_allowance)
+        dq = grads64[len(sources)]
+        expected = oracle_grads(make, sources, q, g.to(torch.bfloat16))[1][len(sources)]
+        compare(results[6 + r], expected, exact=dq, name=f"dq{r}", extra=dq.dq_allowance)
+    for leaf in range(6):
+        bound = accumulated_bound(contributions[leaf], allowances[leaf], roundings=0)
+        check_accumulated(results[leaf], sum(contributions[leaf]), bound, f"leaf{leaf}")

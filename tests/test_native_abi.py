@@ -164,17 +164,20 @@ def test_save_recompute_policy_matches_the_header_and_the_ops():
     text = HEADER.read_text()
     assert f"#define ATTNRES_RECOMPUTE_MAX_SOURCES {_ops.RECOMPUTE_MAX_SOURCES}" in text
     assert f"#define ATTNRES_KEYRES_MAX_SOURCES {_ops.KEYRES_MAX_SOURCES}" in text
-    assert _ops.RECOMPUTE_MAX_SOURCES == 6 and _ops.KEYRES_MAX_SOURCES == 16
+    assert f"#define ATTNRES_KEYRES_FULL_MAX_SOURCES {_ops.KEYRES_FULL_MAX_SOURCES}" in text
+    assert _ops.RECOMPUTE_MAX_SOURCES == 6 and _ops.KEYRES_MAX_SOURCES == 16 and _ops.KEYRES_FULL_MAX_SOURCES == 12
     for count in range(1, 130):
         assert bool(lib.attnres_hip_saves_refinement(count)) == (count > 6)
     key_resident = {(2048, 512), (2048, 1024), (4096, 512), (4096, 1024)}
+    full_key = {(2048, 2048)}
     widths = (1, 8, 64, 100, 512, 1000, 1024, 1536, 2040, 2048, 2056, 3072, 4096, 5000, 8192)
     for width in widths:
         for rank in sorted({1, 8, 256, 511, 512, 513, 768, 1024, 1536, 2048, 3072, width // 2, width} - {0}):
             if rank > width:
                 continue
-            for count in (1, 6, 7, 9, 16, 17, 25, 129):
-                expected = count > 6 and not (count <= 16 and (width, rank) in key_resident)
+            for count in (1, 6, 7, 9, 12, 13, 16, 17, 25, 129):
+                expected = count > 6 and not ((count <= 16 and (width, rank) in key_resident) or
+                                              (count <= 12 and (width, rank) in full_key))
                 assert _ops.saves_refinement(count, width, rank) == expected, (count, width, rank)
                 assert bool(lib.attnres_hip_saves_refinement_for(count, width, rank)) == expected, (count, width, rank)
 
