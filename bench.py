@@ -568,6 +568,7 @@ def sweep_cpu_baseline(cfg: dict, budget_s: float, samples=(1, 12, 24, 48)) -> d
             total_bytes += sum(sum(read_bytes(s, tokens, width)) for s in range(1, max_sources + 1))
             fits.append({"width": width, "rank": rank, "samples_S_s": [[s, round(t, 4)] for s, t in zip(samples, times)],
                          "s_per_step": round(step_s, 3)})
+            print(f"c5 cpu baseline: D={width} R={rank} done", file=sys.stderr, flush=True)
     steps = len(fits)
     return {
         "value": round(total_bytes / total_s / 1e12, 6), "unit": "TB/s",
@@ -632,6 +633,7 @@ def run_sweep(cfg: dict, steps: int, warmup: int, cpu_budget: float | None = Non
                           "bytes_per_step": step_bytes, "per_read_S_us_TBs": per_read})
             total_bytes += step_bytes
             total_ms += step_ms
+            print(f"c5 sweep: D={width} R={rank} done, {step_ms:.2f} ms per step", file=sys.stderr, flush=True)
     value = total_bytes / (total_ms * 1e-3) / 1e12
     return {
         "metric": "c5 24-layer full-schedule sweep: summed operator fwd+bwd time per step (48 reads) and TB/s",
