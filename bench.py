@@ -504,7 +504,8 @@ def run_block_schedule(cfg: dict, steps: int, warmup: int, cpu_budget: float | N
                        "speedup": round(plain_ms / shared_ms, 3),
                        "what": "forward of the 3 reads + one autograd.grad over them; SharedSources sums "
                                "the source gradients in the backward kernels"},
-        "roofline": {"bound": "hbm", "kernel": "backward op (list layout)", "achieved": round(bwd_tbs * 1e3, 1),
+        "roofline": {"bound": "hbm", "achieved": round(bwd_tbs * 1e3, 1),
+                     "kernel": f"backward op (list layout): {backward_kernel(cfg['sources'], width, rank)} + attnres_dq_reduce_kernel",
                      "peak": HBM_PEAK_TBS * 1e3, "unit": "GB/s", "frac": round(bwd_tbs / HBM_PEAK_TBS, 4),
                      "traffic": measured_traffic("c4", "backward_bytes")},
         "cpu_baseline": (None if cpu_budget is None else
@@ -538,6 +539,20 @@ def _sweep_one_backward_pass(values, query, grad_out, max_sources: int, steps: i
     stop.record()
     torch.cuda.synchronize()
     return start.elapsed_time(stop) / steps
+
+
+def backward_kernel(sources: int, width: int, rank: int) -> str:
+    """The backward kernel the library launches for a plain read of this shape
+    (the save/recompute policy, then the token-block choice for 2048-wide rows)."""
+    from attnres import _ops
+
+    if sources <= _ops.RECOMPUTE_MAX_SOURCES:
+        return "attnres_bwd_recompute_kernel"
+    if not _ops.saves_refinement(sources, width, rank):
+        return "attnres_bwd_keyres_kernel"
+    if sources >= 13 and width == rank == 2048:
+        return "attnres_bwd_block_kernel"
+    return "attnres_bwd_kernel"
 
 
 def sweep_cpu_baseline(cfg: dict, budget_s: float, samples=(1, 12, 24, 48)) -> dict:
@@ -1041,8 +1056,7 @@ def main(argv=None) -> int:
         "backward": {"us": round(bwd_avg * 1e3, 2), "bytes": bwd_bytes, "TB/s": round(bwd_tbs, 4),
                      "pct_of_peak": round(100 * bwd_tbs / HBM_PEAK_TBS, 2)},
         "roofline": {"bound": "hbm",
-                     "kernel": ("backward op: " + ("attnres_bwd_block_kernel" if sources >= 13 and width == cfg["rank"] == 2048
-                                                  else "attnres_bwd_kernel") + " + attnres_dq_reduce_kernel"),
+                     "kernel": f"backward op: {backward_kernel(sources, width, cfg['rank'])} + attnres_dq_reduce_kernel",
                      "achieved": round(bwd_tbs * 1e3, 1), "peak": HBM_PEAK_TBS * 1e3,
                      "unit": "GB/s", "frac": round(bwd_tbs / HBM_PEAK_TBS, 4),
                      "traffic": measured_traffic(args.config, "backward_bytes")},

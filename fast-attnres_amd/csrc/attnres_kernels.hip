@@ -1420,7 +1420,7 @@ __global__ void __launch_bounds__(kBlock) attnres_bwd_recompute_kernel(const Bwd
 // Group = one wavefront (G = 64).  Grid-stride over tokens like the streaming
 // kernel; NB value rows in flight in a ring that crosses token boundaries.
 // Items are counted per token with S rounded up to a multiple of NB (an item
-// past S loads the idle row and does nothing), so slot j always serves items
+// past S is padding and does nothing), so slot j always serves items
 // j, j + NB, ... and every register index is a compile-time constant.  The
 // next token's dO and statistics are requested two items before the token
 // ends.
@@ -1463,14 +1463,29 @@ attnres_bwd_keyres_kernel(const BwdArgs<Rows, Grads> a) {
     float run_max = a.stats[token], inv_sum = a.stats[a.n_tokens + token];
     float pend_max = run_max, pend_sum = inv_sum;
     load_row<G, CH, VEC>(a.grad_out + token * D, lane, D, g);
-    const uint16_t* idle = a.src.row(0, token);
-    u32x4 ring[NB][CH];
-    float ring_z[NB], ring_r[NB];
+    // A padding item (past S, or past the group's last token) is never
+    // consumed.  For 4096-wide rows it loads nothing (a uniform branch); for
+    // 2048-wide rows it loads a row that is already cached: with a key of 2 or
+    // 4 columns one row shared by every group, which stays in L2 (the group's
+    // own first row is evicted between uses and re-read from HBM), with a key
+    // of one column the group's first row, as measured fastest (see the
+    // launcher).
+    const uint16_t* idle = KC >= 2 ? a.src.row(0, 0) : a.src.row(0, token);
+    u32x4 ring[NB][CH] = {};
+    float ring_z[NB] = {}, ring_r[NB] = {};
     auto load_item = [&](int j, int64_t tok, int s, bool live) __attribute__((always_inline)) {
-      load_row<G, CH, VEC>(live ? a.src.row(s, tok) : idle, lane, D, ring[j]);
-      const int64_t item = live ? tok * S + s : 0;
-      ring_z[j] = a.logit[item];
-      ring_r[j] = a.inv_rms[item];
+      if constexpr (CH == 8) {
+        if (live) {
+          load_row<G, CH, VEC>(a.src.row(s, tok), lane, D, ring[j]);
+          ring_z[j] = a.logit[tok * S + s];
+          ring_r[j] = a.inv_rms[tok * S + s];
+        }
+      } else {
+        load_row<G, CH, VEC>(live ? a.src.row(s, tok) : idle, lane, D, ring[j]);
+        const int64_t item = live ? tok * S + s : 0;
+        ring_z[j] = a.logit[item];
+        ring_r[j] = a.inv_rms[item];
+      }
     };
 #pragma unroll
     for (int j = 0; j < NB; ++j) load_item(j, token, j, j < S);
@@ -2082,6 +2097,21 @@ int64_t launch_bwd_recompute(const BwdArgs<Rows, Grads>& a, hipStream_t stream) 
 // refinement -> key-resident, D = R = 2048): S = 9, N = 32768 (c4's shape):
 // 722.1 -> 698.7; S = 7: 299.7 -> 291.6; S = 12: 459.0 -> 446.7; S = 9,
 // N = 16384: 358.6 -> 352.4.
+//
+// Padding items (S odd, and the items past a group's last token) first
+// re-read the group's first row, which the stream had evicted from L2 by then:
+// 4.4% extra HBM reads at c4's shape (rocprofv3 FETCH_SIZE).  Measured on
+// MI355X (fwd + bwd per read, us; that row -> no load for 4096-wide rows, one
+// row shared by all groups for 2048-wide rows): S = 16, D = 4096, R = 1024
+// (c3): 1196.0 -> 1166.9 (the backward 825.8 -> 795.3, although c3 pads
+// only past a group's last token: the branch changes the compiled schedule);
+// S = 15: 1140.8 -> 1100.2; S = 7:
+// 578.8 -> 539.0; S = 13, R = 512: 998.0 -> 958.2; S = 9, N = 32768,
+// D = R = 2048 (c4's shape): 699.0 -> 680.7; S = 11, D = R = 2048: 419.3 ->
+// 411.9; S = 12: 449.7 -> 445.0; S = 11, D = 2048, R = 1024: 433.3 -> 428.6.
+// Skipping the load for 2048-wide rows was slower (c4's shape 708.4, S = 12
+// 472.3), and the shared row at S = 16, D = 2048, R = 512 too (593.0 ->
+// 604.1), so that key keeps the group's first row.
 template <int G, int CH, int KC, bool VEC, class Rows, class Grads>
 int64_t launch_bwd_keyres_chunks(const BwdArgs<Rows, Grads>& a, hipStream_t stream) {
   constexpr int NB = 2;

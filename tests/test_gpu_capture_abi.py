@@ -113,6 +113,7 @@ def test_abi_calls_replay_from_a_hip_graph(layout):
         buffers.enqueue(handle)  # eager reference (also warms the occupancy caches)
     torch.cuda.synchronize()
     eager = [t.clone() for t in buffers.outputs()]
+    torch.cuda.synchronize()  # the clones (default stream) finish before the replays zero the outputs (side stream)
 
     graph, exec_ = ctypes.c_void_p(), ctypes.c_void_p()
     assert hip.hipStreamBeginCapture(handle, _CAPTURE_MODE_RELAXED) == 0
@@ -180,9 +181,8 @@ def test_no_alloc_backward_replays_from_a_hip_graph(shape):
             with torch.cuda.stream(side):
                 grad_out.copy_(torch.randn(tokens, width, device=dev).to(torch.bfloat16))
             call()  # eager on the new inputs
-            assert hip.hipStreamSynchronize(handle) == 0
-            eager = (dv.clone(), dq.clone())
-            with torch.cuda.stream(side):
+            with torch.cuda.stream(side):  # snapshot and clear in stream order
+                eager = (dv.clone(), dq.clone())
                 dv.zero_()
                 dq.zero_()
             assert hip.hipGraphLaunch(exec_, handle) == 0
