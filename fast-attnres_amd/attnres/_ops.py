@@ -183,49 +183,81 @@ def _dq_workspace(lib, n_tokens: int, width: int, rank: int, device) -> Tensor:
     return torch.empty((elems,), device=device, dtype=_F32)
 
 
+def _pool_layout(tokens: int, sources: int, width: int, save: bool) -> tuple[int, int, int]:
+    """``(head, block, size)`` of a pooled saved state: the refinement bytes
+    ``[N, D]`` (when saved) at offset 0, then from the 16-byte aligned byte
+    offset ``head`` logit ``[N, S]``, 1/rms ``[N, S]`` (``block`` = N*S floats
+    each) and stats ``[2, N]`` in FP32; ``size`` bytes in all."""
+    head = ((tokens * width if save else 0) + 15) // 16 * 16
+    block = tokens * sources
+    return head, block, head + 4 * (2 * block + 2 * tokens)
+
+
 def _saved_state(tokens: int, sources: int, width: int, save: bool, device,
                  pooled: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """out_refine ``[N, D]`` int8 (``[0, D]`` when not saved), logit ``[N, S]``,
     inv_rms ``[N, S]`` and stats ``[2, N]`` (FP32).  ``pooled``: views of one
-    byte allocation, for callers that keep them together (not for custom-op
-    outputs, which must not alias each other); a small read then pays one
-    allocation here instead of four."""
+    byte allocation (``_pool_layout``), for callers that keep them together
+    (not for custom-op outputs, which must not alias each other); a small read
+    then pays one allocation here instead of four."""
     refine_rows = tokens if save else 0
     if not pooled:
         return (torch.empty((refine_rows, width), device=device, dtype=torch.int8),
                 torch.empty((tokens, sources), device=device, dtype=_F32),
                 torch.empty((tokens, sources), device=device, dtype=_F32),
                 torch.empty((2, tokens), device=device, dtype=_F32))
-    block = tokens * sources
-    head = (refine_rows * width + 15) // 16 * 16  # the FP32 part starts 16-byte aligned
-    pool = torch.empty((head + 4 * (2 * block + 2 * tokens),), device=device, dtype=torch.uint8)
+    head, block, size = _pool_layout(tokens, sources, width, save)
+    pool = torch.empty((size,), device=device, dtype=torch.uint8)
     floats = pool[head:].view(_F32)
     return (pool[:refine_rows * width].view(torch.int8).view(refine_rows, width),
             floats[:block].view(tokens, sources), floats[block:2 * block].view(tokens, sources),
             floats[2 * block:].view(2, tokens))
 
 
+def _pool_addresses(pool: Tensor, tokens: int, sources: int, width: int,
+                    save: bool) -> tuple[int | None, int, int, int]:
+    """Device addresses of (out_refine or None, logit, inv_rms, stats) in a
+    pool laid out by ``_pool_layout``: the eager reads pass these to the
+    library instead of building four views (about 5 us per read)."""
+    head, block, _ = _pool_layout(tokens, sources, width, save)
+    base = pool.data_ptr()
+    logit = base + head
+    return (base if save else None), logit, logit + 4 * block, logit + 8 * block
+
+
+def _state_addresses(out_refine: Tensor, logit: Tensor, inv_rms: Tensor,
+                     stats: Tensor) -> tuple[int | None, int, int, int]:
+    return (_pointer(_contiguous(out_refine)), _contiguous(logit).data_ptr(), _contiguous(inv_rms).data_ptr(),
+            _contiguous(stats).data_ptr())
+
+
 # ------------------------------------------------------------------ packed
+
+def _packed_forward_launch(values: Tensor, query: Tensor, eps: float, scale: float, out: Tensor,
+                           state: tuple[int | None, int, int, int]) -> None:
+    """``attnres_hip_packed_forward`` into ``out`` and the saved state at
+    ``state`` = (out_refine or None, logit, inv_rms, stats) addresses."""
+    sources, tokens, width = (int(size) for size in values.shape)
+    device = values.device
+    with _on_device(device):
+        status = _native.load().attnres_hip_packed_forward(
+            values.data_ptr(), values.stride(0), values.stride(1), sources, tokens, width,
+            query.data_ptr(), query.numel(), eps, scale, out.data_ptr(), *state, _stream(device))
+    _native.check(status, "attnres packed forward")
+
 
 def packed_forward_impl(values: Tensor, query: Tensor, eps: float, scale: float,
                         save: bool, pooled: bool = False) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """The packed forward launch; ``save`` chooses whether the refinement is
     stored (``out_refine`` ``[N, D]``) or not (``[0, D]``); ``pooled`` as for
     ``_saved_state``."""
-    lib = _native.load()
     values = _unit_feature_stride(values)
     query = _contiguous(query)
     sources, tokens, width = (int(size) for size in values.shape)
-    device = values.device
-    out = torch.empty((tokens, width), device=device, dtype=_BF16)
-    out_refine, logit, inv_rms, stats = _saved_state(tokens, sources, width, save, device, pooled)
-    with _on_device(device):
-        status = lib.attnres_hip_packed_forward(
-            values.data_ptr(), values.stride(0), values.stride(1), sources, tokens, width,
-            query.data_ptr(), query.numel(), eps, scale, out.data_ptr(), _pointer(out_refine),
-            logit.data_ptr(), inv_rms.data_ptr(), stats.data_ptr(), _stream(device))
-    _native.check(status, "attnres packed forward")
-    return out, out_refine, logit, inv_rms, stats
+    out = torch.empty((tokens, width), device=values.device, dtype=_BF16)
+    state = _saved_state(tokens, sources, width, save, values.device, pooled)
+    _packed_forward_launch(values, query, eps, scale, out, _state_addresses(*state))
+    return (out, *state)
 
 
 @torch.library.custom_op("attnres_hip::packed_forward", mutates_args=(),
@@ -246,16 +278,16 @@ def _packed_forward_fake(values, query, eps, scale):
             values.new_empty((2, tokens), dtype=_F32))
 
 
-def packed_backward_impl(values: Tensor, query: Tensor, out: Tensor, out_refine: Tensor,
-                         grad_out: Tensor, logit: Tensor, inv_rms: Tensor, stats: Tensor,
-                         scale: float) -> tuple[Tensor, Tensor]:
-    """The packed backward launch (dv rows and dq)."""
+def _packed_backward_launch(values: Tensor, query: Tensor, out: Tensor | None, grad_out: Tensor,
+                            state: tuple[int | None, int, int, int], scale: float) -> tuple[Tensor, Tensor]:
+    """``attnres_hip_packed_backward`` with the saved state at ``state``
+    addresses (out_refine None: nothing saved, delta from the value rows; then
+    ``out`` is not read)."""
     lib = _native.load()
     values = _unit_feature_stride(values)
     query = _contiguous(query)
-    out = _contiguous(out)
     grad_out = _contiguous(grad_out.to(_BF16))
-    recompute = out_refine.numel() == 0  # nothing saved: delta from the value rows
+    refine = state[0]
     sources, tokens, width = (int(size) for size in values.shape)
     rank = query.numel()
     device = values.device
@@ -265,13 +297,20 @@ def packed_backward_impl(values: Tensor, query: Tensor, out: Tensor, out_refine:
     with _on_device(device):
         status = lib.attnres_hip_packed_backward(
             values.data_ptr(), values.stride(0), values.stride(1), sources, tokens, width,
-            query.data_ptr(), rank, scale, None if recompute else out.data_ptr(),
-            None if recompute else _contiguous(out_refine).data_ptr(),
-            grad_out.data_ptr(), _contiguous(logit).data_ptr(), _contiguous(inv_rms).data_ptr(),
-            _contiguous(stats).data_ptr(), grad_values.data_ptr(), grad_query.data_ptr(),
+            query.data_ptr(), rank, scale, None if refine is None else _contiguous(out).data_ptr(), refine,
+            grad_out.data_ptr(), *state[1:], grad_values.data_ptr(), grad_query.data_ptr(),
             workspace.data_ptr(), workspace.numel(), _stream(device))
     _native.check(status, "attnres packed backward")
     return grad_values, grad_query
+
+
+def packed_backward_impl(values: Tensor, query: Tensor, out: Tensor, out_refine: Tensor,
+                         grad_out: Tensor, logit: Tensor, inv_rms: Tensor, stats: Tensor,
+                         scale: float) -> tuple[Tensor, Tensor]:
+    """The packed backward launch (dv rows and dq); an empty ``out_refine``
+    means nothing was saved (delta from the value rows)."""
+    return _packed_backward_launch(values, query, out, grad_out,
+                                   _state_addresses(out_refine, logit, inv_rms, stats), scale)
 
 
 @torch.library.custom_op("attnres_hip::packed_backward", mutates_args=(),
@@ -323,23 +362,35 @@ class _PackedRead(torch.autograd.Function):
     """The packed read in eager mode: the same launches, saved state and
     gradients as the ``packed_forward`` op with its registered autograd, without
     going through the op dispatcher (tens of microseconds per read, which bound
-    small reads)."""
+    small reads).  It returns the output alone and keeps the saved state (the
+    refinement and the statistics) in one byte allocation whose addresses it
+    passes to the library: four non-differentiable outputs, or four views of
+    the pool, would cost the host about 20 us per read."""
 
     @staticmethod
     def forward(ctx, values: Tensor, query: Tensor, eps: float, scale: float):
-        outputs = packed_forward_impl(values, query, eps, scale,
-                                      saves_refinement(int(values.shape[0]), int(values.shape[-1]), query.numel()),
-                                      pooled=True)
-        _packed_setup_context(ctx, (values, query, eps, scale), outputs)
-        return outputs
+        flat = _unit_feature_stride(values)
+        dense_query = _contiguous(query)
+        sources, tokens, width = (int(size) for size in flat.shape)
+        save = saves_refinement(sources, width, dense_query.numel())
+        out = torch.empty((tokens, width), device=flat.device, dtype=_BF16)
+        pool = torch.empty((_pool_layout(tokens, sources, width, save)[2],), device=flat.device, dtype=torch.uint8)
+        _packed_forward_launch(flat, dense_query, eps, scale, out, _pool_addresses(pool, tokens, sources, width, save))
+        ctx.set_materialize_grads(False)
+        ctx.save_for_backward(values, query, pool, *((out,) if save else ()))
+        ctx.save = save
+        ctx.scale = float(scale)
+        return out
 
     @staticmethod
-    def backward(ctx, grad_out, *_aux_grads):
+    def backward(ctx, grad_out):
         if grad_out is None:
             return None, None, None, None
-        values, query, out, out_refine, logit, inv_rms, stats = ctx.saved_tensors
-        grad_values, grad_query = packed_backward_impl(values, query, out, out_refine, grad_out, logit, inv_rms,
-                                                       stats, ctx.scale)
+        values, query, pool, *out = ctx.saved_tensors
+        sources, tokens, width = (int(size) for size in values.shape)
+        state = _pool_addresses(pool, tokens, sources, width, ctx.save)
+        grad_values, grad_query = _packed_backward_launch(values, query, out[0] if out else None, grad_out, state,
+                                                          ctx.scale)
         return (grad_values if ctx.needs_input_grad[0] else None,
                 grad_query if ctx.needs_input_grad[1] else None, None, None)
 
@@ -354,8 +405,8 @@ def packed_attnres(values: Tensor, query: Tensor, eps: float, scale: float) -> T
     if width > 1 and flat.stride(2) != 1:
         flat = flat.contiguous()
     query = _contiguous(query)
-    read = _PackedRead.apply if _eager(flat, query) else packed_forward
-    out = read(flat, query, eps, scale)[0]
+    out = _PackedRead.apply(flat, query, eps, scale) if _eager(flat, query) else packed_forward(flat, query, eps,
+                                                                                                 scale)[0]
     return out.reshape(values.shape[1:])
 
 
@@ -373,26 +424,33 @@ def _source_table(sources: list[Tensor]) -> tuple[list[Tensor], Any, Any]:
     return prepared, pointers, row_strides
 
 
+def _sources_forward_launch(sources: list[Tensor], query: Tensor, eps: float, scale: float, out: Tensor,
+                            state: tuple[int | None, int, int, int]) -> None:
+    """``attnres_hip_sources_forward`` into ``out`` and the saved state at
+    ``state`` addresses (as ``_packed_forward_launch``)."""
+    first = sources[0]
+    count, tokens, width = len(sources), _rows_of(first.shape), int(first.shape[-1])
+    device = first.device
+    prepared, pointers, row_strides = _source_table(sources)
+    with _on_device(device):
+        status = _native.load().attnres_hip_sources_forward(
+            pointers, row_strides, count, tokens, width, query.data_ptr(), query.numel(),
+            eps, scale, out.data_ptr(), *state, _stream(device))
+    del prepared  # copies (if any) stay alive until the launch is enqueued
+    _native.check(status, "attnres source-list forward")
+
+
 def sources_forward_impl(sources: list[Tensor], query: Tensor, eps: float, scale: float,
                          save: bool, pooled: bool = False) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """The source-list forward launch; ``save`` and ``pooled`` as for
     ``packed_forward_impl``."""
-    lib = _native.load()
     first = sources[0]
     query = _contiguous(query)
     count, tokens, width = len(sources), _rows_of(first.shape), int(first.shape[-1])
-    device = first.device
-    prepared, pointers, row_strides = _source_table(sources)
-    out = torch.empty(first.shape, device=device, dtype=_BF16)
-    out_refine, logit, inv_rms, stats = _saved_state(tokens, count, width, save, device, pooled)
-    with _on_device(device):
-        status = lib.attnres_hip_sources_forward(
-            pointers, row_strides, count, tokens, width, query.data_ptr(), query.numel(),
-            eps, scale, out.data_ptr(), _pointer(out_refine), logit.data_ptr(),
-            inv_rms.data_ptr(), stats.data_ptr(), _stream(device))
-    del prepared  # copies (if any) stay alive until the launch is enqueued
-    _native.check(status, "attnres source-list forward")
-    return out, out_refine, logit, inv_rms, stats
+    out = torch.empty(first.shape, device=first.device, dtype=_BF16)
+    state = _saved_state(tokens, count, width, save, first.device, pooled)
+    _sources_forward_launch(sources, query, eps, scale, out, _state_addresses(*state))
+    return (out, *state)
 
 
 @torch.library.custom_op("attnres_hip::sources_forward", mutates_args=(),
@@ -415,16 +473,16 @@ def _sources_forward_fake(sources, query, eps, scale):
             first.new_empty((2, tokens), dtype=_F32))
 
 
-def sources_backward_impl(sources: list[Tensor], query: Tensor, out: Tensor, out_refine: Tensor,
-                          grad_out: Tensor, logit: Tensor, inv_rms: Tensor, stats: Tensor,
-                          scale: float) -> list[Tensor]:
-    """The source-list backward launch: one dv buffer per list position, then dq."""
+def _sources_backward_launch(sources: list[Tensor], query: Tensor, out: Tensor | None, grad_out: Tensor,
+                             state: tuple[int | None, int, int, int], scale: float) -> list[Tensor]:
+    """``attnres_hip_sources_backward`` with the saved state at ``state``
+    addresses (as ``_packed_backward_launch``): one dv buffer per list
+    position, then dq."""
     lib = _native.load()
     first = sources[0]
     query = _contiguous(query)
-    out = _contiguous(out)
     grad_out = _contiguous(grad_out.to(_BF16))
-    recompute = out_refine.numel() == 0
+    refine = state[0]
     count, tokens, width = len(sources), _rows_of(first.shape), int(first.shape[-1])
     rank = query.numel()
     device = first.device
@@ -436,13 +494,19 @@ def sources_backward_impl(sources: list[Tensor], query: Tensor, out: Tensor, out
     with _on_device(device):
         status = lib.attnres_hip_sources_backward(
             pointers, row_strides, count, tokens, width, query.data_ptr(), rank, scale,
-            None if recompute else out.data_ptr(), None if recompute else _contiguous(out_refine).data_ptr(),
-            grad_out.data_ptr(), _contiguous(logit).data_ptr(),
-            _contiguous(inv_rms).data_ptr(), _contiguous(stats).data_ptr(), grad_pointers,
-            grad_query.data_ptr(), workspace.data_ptr(), workspace.numel(), _stream(device))
+            None if refine is None else _contiguous(out).data_ptr(), refine, grad_out.data_ptr(), *state[1:],
+            grad_pointers, grad_query.data_ptr(), workspace.data_ptr(), workspace.numel(), _stream(device))
     del prepared
     _native.check(status, "attnres source-list backward")
     return [*grads, grad_query]
+
+
+def sources_backward_impl(sources: list[Tensor], query: Tensor, out: Tensor, out_refine: Tensor,
+                          grad_out: Tensor, logit: Tensor, inv_rms: Tensor, stats: Tensor,
+                          scale: float) -> list[Tensor]:
+    """The source-list backward launch: one dv buffer per list position, then dq."""
+    return _sources_backward_launch(sources, query, out, grad_out,
+                                    _state_addresses(out_refine, logit, inv_rms, stats), scale)
 
 
 @torch.library.custom_op("attnres_hip::sources_backward", mutates_args=(),
@@ -492,21 +556,32 @@ class _SourcesRead(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, query: Tensor, eps: float, scale: float, *sources: Tensor):
-        outputs = sources_forward_impl(list(sources), query, eps, scale,
-                                       saves_refinement(len(sources), int(sources[0].shape[-1]), query.numel()),
-                                       pooled=True)
-        _sources_setup_context(ctx, (sources, query, eps, scale), outputs)
-        return outputs
+        first = sources[0]
+        dense_query = _contiguous(query)
+        count, tokens, width = len(sources), _rows_of(first.shape), int(first.shape[-1])
+        save = saves_refinement(count, width, dense_query.numel())
+        out = torch.empty(first.shape, device=first.device, dtype=_BF16)
+        pool = torch.empty((_pool_layout(tokens, count, width, save)[2],), device=first.device, dtype=torch.uint8)
+        _sources_forward_launch(list(sources), dense_query, eps, scale, out,
+                                _pool_addresses(pool, tokens, count, width, save))
+        ctx.set_materialize_grads(False)
+        ctx.save_for_backward(*sources, query, pool, *((out,) if save else ()))
+        ctx.count = count
+        ctx.save = save
+        ctx.scale = float(scale)
+        return out
 
     @staticmethod
-    def backward(ctx, grad_out, *_aux_grads):
+    def backward(ctx, grad_out):
         count = ctx.count
         if grad_out is None:
             return (None, None, None, *([None] * count))
         saved = ctx.saved_tensors
-        query, out, out_refine, logit, inv_rms, stats = saved[count:]
-        grads = sources_backward_impl(list(saved[:count]), query, out, out_refine, grad_out, logit, inv_rms,
-                                      stats, ctx.scale)
+        sources = list(saved[:count])
+        query, pool, *out = saved[count:]
+        first = sources[0]
+        state = _pool_addresses(pool, _rows_of(first.shape), count, int(first.shape[-1]), ctx.save)
+        grads = _sources_backward_launch(sources, query, out[0] if out else None, grad_out, state, ctx.scale)
         return (grads[count] if ctx.needs_input_grad[0] else None, None, None, *grads[:count])
 
 
@@ -516,7 +591,7 @@ def sources_attnres(sources: tuple[Tensor, ...], query: Tensor, eps: float,
     `fixed_tail_sources.py:186-195`): the list is passed through unpacked."""
     query = _contiguous(query)
     if _eager(query, *sources):
-        return _SourcesRead.apply(query, eps, scale, *sources)[0]
+        return _SourcesRead.apply(query, eps, scale, *sources)
     return sources_forward(list(sources), query, eps, scale)[0]
 
 
