@@ -257,3 +257,28 @@ def test_eager_path_choice():
     with FakeTensorMode():
         fake = torch.empty(3)
     assert not _ops._eager(plain, fake)
+
+
+@pytest.mark.parametrize("save", [False, True])
+@pytest.mark.parametrize("tokens,sources,width", [(1, 1, 1), (7, 9, 33), (300, 25, 2048), (5, 129, 8192)])
+def test_pooled_saved_state_layout(tokens, sources, width, save):
+    """The eager read keeps its saved state in one byte pool and passes the
+    library addresses computed by ``_pool_addresses``; the pooled views of
+    ``_saved_state`` must sit at exactly those addresses, 16-byte aligned past
+    the refinement, without overlap and inside the pool."""
+    ops = _ops()
+    refine, logit, inv_rms, stats = ops._saved_state(tokens, sources, width, save, "cpu", pooled=True)
+    base = refine.untyped_storage().data_ptr()
+    head, block, size = ops._pool_layout(tokens, sources, width, save)
+    assert refine.untyped_storage().nbytes() == size
+    assert refine.shape == ((tokens if save else 0), width) and logit.shape == inv_rms.shape == (tokens, sources)
+    assert stats.shape == (2, tokens)
+    pool = torch.empty(0, dtype=torch.uint8).set_(refine.untyped_storage())
+    addresses = ops._pool_addresses(pool, tokens, sources, width, save)
+    assert addresses == ((refine.data_ptr() if save else None), logit.data_ptr(), inv_rms.data_ptr(),
+                         stats.data_ptr())
+    spans = [(t.data_ptr(), t.data_ptr() + t.numel() * t.element_size())
+             for t in (refine, logit, inv_rms, stats) if t.numel()]  # an empty view reports address 0
+    assert all(base <= lo <= hi <= base + size for lo, hi in spans)
+    assert all(a[1] <= b[0] for a, b in zip(spans, spans[1:]))
+    assert (logit.data_ptr() - base) % 16 == 0 and head >= (tokens * width if save else 0)

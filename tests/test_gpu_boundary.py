@@ -190,3 +190,47 @@ def test_the_guard_catches_a_stacked_read():
     with pytest.raises(AssertionError, match="stacked its sources"):
         with SourceStackGuard([leaf.shape for leaf in leaves], 3):
             oracle(tuple(leaves), query)
+
+
+# ------------------------------------------- eager Function against the ops
+
+@pytest.mark.parametrize("layout", ["packed", "list"])
+@pytest.mark.parametrize("shape", [(5, 300, 1024, 1024), (9, 257, 1024, 256), (9, 300, 2048, 2048),
+                                   (16, 300, 4096, 1024), (25, 300, 2048, 2048)],
+                         ids=["recompute", "saved", "key-resident-row", "key-resident-key", "saved-block"])
+def test_eager_function_matches_the_ops_bit_for_bit(layout, shape):
+    """In eager mode a read runs through a direct autograd.Function that keeps
+    its saved state in one pooled allocation and passes addresses to the
+    library; the registered ops (used under torch.compile) allocate each
+    saved tensor apart.  Both must launch the same kernels on the same
+    state: out, dv and dq bit-identical, on every backward path (recompute,
+    saved refinement, key-resident with a partial and a whole-row key, token
+    blocks)."""
+    sources, tokens, width, rank = shape
+    torch.manual_seed(3)
+    print(f"eager vs ops {layout} S,N,D,R={shape}", flush=True)
+    values = torch.randn(sources, tokens, width, device="cuda").to(torch.bfloat16)
+    query = (torch.randn(rank, device="cuda") / rank ** 0.5).to(torch.bfloat16)
+    upstream = torch.randn(tokens, width, device="cuda").to(torch.bfloat16)
+    from attnres import _ops  # noqa: F401  (registers the ops)
+
+    if layout == "packed":
+        leaf = values.clone().requires_grad_()
+        q = query.clone().requires_grad_()
+        out = attnres(leaf, q)
+        eager = (out, *torch.autograd.grad(out, (leaf, q), upstream))
+        saved = torch.ops.attnres_hip.packed_forward(values, query, 2**-23, 1.0)
+        grads = torch.ops.attnres_hip.packed_backward(values, query, saved[0], saved[1], upstream, *saved[2:], 1.0)
+        ops = (saved[0], *grads)
+    else:
+        leaves = [values[s].clone().requires_grad_() for s in range(sources)]
+        q = query.clone().requires_grad_()
+        out = attnres(leaves, q)
+        grads = torch.autograd.grad(out, (*leaves, q), upstream)
+        eager = (out, torch.stack(grads[:-1]), grads[-1])
+        listed = list(values.unbind(0))
+        saved = torch.ops.attnres_hip.sources_forward(listed, query, 2**-23, 1.0)
+        grads = torch.ops.attnres_hip.sources_backward(listed, query, saved[0], saved[1], upstream, *saved[2:], 1.0)
+        ops = (saved[0], torch.stack(grads[:-1]), grads[-1])
+    for name, a, b in zip(("out", "dv", "dq"), eager, ops):
+        assert torch.equal(a, b), f"{name} differs between the eager Function and the ops"
