@@ -36,6 +36,7 @@ PAIRS = [
     ((4, 3000, 4096, 1024), (2, 17, 96, 40)),          # recompute (wide groups), then a tiny read
     ((25, 16384, 2048, 2048), (13, 4096, 2048, 2048)),  # c2: the token-block grid cut to 511 rows, then uncut
     ((16, 8192, 4096, 1024), (9, 999, 2048, 512)),     # key-resident backward, both widths
+    ((12, 16384, 2048, 2048), (7, 999, 2048, 2048)),   # key-resident, the whole row as key (grid cut, then not)
 ]
 CUT_EXPECTED = {(25, 16384, 2048, 2048)}  # shapes whose launch must exceed the array's rows on an MI355X
 
