@@ -151,6 +151,46 @@ def test_key_resident_backward_matches_oracle(sources, width, rank, padded, layo
     check_statistics(make([producer.detach()], query)[0], query.detach())
 
 
+def _random_keyres_cases(count: int, seed: int = 20261202) -> list[tuple]:
+    """Reads the key-resident backward takes, drawn at random: every key
+    shape, any source count it accepts, token counts from 1 to 1500 (odd ones,
+    and fewer than a grid's token groups, leave groups idle or with one token
+    and put padding items at every group's end), aligned or padded rows,
+    packed or list."""
+    import random
+
+    rng = random.Random(seed)
+    shapes = KEYRES_SHAPES + [(2048, 2048)]
+    cases = []
+    for _ in range(count):
+        width, rank = rng.choice(shapes)
+        top = _ops.KEYRES_FULL_MAX_SOURCES if width == rank else _ops.KEYRES_MAX_SOURCES
+        sources = rng.randint(_ops.RECOMPUTE_MAX_SOURCES + 1, top)
+        tokens = rng.choice([1, 2, 3, rng.randint(4, 200), rng.randint(200, 1500) | 1])
+        cases.append((sources, tokens, width, rank, rng.random() < 0.3, rng.choice(["packed", "list"])))
+    return cases
+
+
+@pytest.mark.parametrize("sources,tokens,width,rank,padded,layout", _random_keyres_cases(24), ids=lambda v: str(v))
+def test_key_resident_random_shapes_match_oracle(sources, tokens, width, rank, padded, layout):
+    """Random key-resident reads against the oracle at the full bars (no delta
+    allowance)."""
+    assert not _ops.saves_refinement(sources, width, rank)
+    producer, query, upstream = _inputs(sources, tokens, width, rank, padded, SEEDS[2] + 17 + sources * tokens + width)
+
+    def make(leaves, q):
+        values = leaves[0][..., :width]
+        return (tuple(values.unbind(0)) if layout == "list" else values), q
+
+    print(f"key-resident random S={sources} N={tokens} D={width} R={rank} padded={padded} {layout}", flush=True)
+    set_case(f"key-resident random S={sources} N={tokens} D={width} R={rank} padded={padded} {layout}")
+    actual = attnres(make([producer], query)[0], query)
+    grads = torch.autograd.grad(actual, (producer, query), upstream)
+    expected, exact = both_oracles(make, [producer], query, upstream)
+    torch.cuda.synchronize()
+    compare_read((actual, *grads), expected, exact, ["out", "dv", "dq"], sources=sources)
+
+
 @pytest.mark.parametrize("layout", ["packed", "list"])
 @pytest.mark.parametrize("sources,tokens,width,rank",
                          [(s, n, w, r) for s, n in ((7, 5003), (16, 2053), (9, 1)) for w, r in KEYRES_SHAPES] +
