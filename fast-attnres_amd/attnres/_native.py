@@ -1,19 +1,25 @@
-"""ctypes binding of the C ABI in `include/attnres_hip.h`.
+"""ctypes binding of the C ABI in `include/attnres_hip.h`, and the loader of
+the eager autograd nodes.
 
 The shared library `_lib/libattnres_hip.so` is built in-tree from
-`csrc/attnres_hip.hip` by `build_native.py` (hipcc, gfx950).  There is no
-fallback: if the library is missing or does not load, every operator call
-raises, so a GPU run can never silently take another path.
+`csrc/attnres_hip.hip` by `build_native.py` (hipcc, gfx950), and so is
+`_lib/_autograd.so` (`csrc/attnres_autograd.cpp`, a PyTorch C++ extension
+linked to that library).  There is no fallback: if either is missing or does
+not load, every operator call raises, so a GPU run can never silently take
+another path.
 """
 
 from __future__ import annotations
 
 import ctypes
+import importlib.util
 import threading
 from pathlib import Path
+from types import ModuleType
 
 LIBRARY_NAME = "libattnres_hip.so"
 LIBRARY_PATH = Path(__file__).resolve().parent / "_lib" / LIBRARY_NAME
+AUTOGRAD_PATH = Path(__file__).resolve().parent / "_lib" / "_autograd.so"
 
 # Status codes of `enum attnres_status`.
 OK = 0
@@ -111,6 +117,35 @@ def load() -> ctypes.CDLL:
     return _library
 
 
+_autograd: ModuleType | None = None
+
+
+def load_autograd() -> ModuleType:
+    """Load (once) and return the eager autograd nodes (`packed_read`,
+    `sources_read`), or raise RuntimeError.  The HIP library is loaded first:
+    the module links it, and both then share one copy of its state."""
+    global _autograd
+    if _autograd is not None:
+        return _autograd
+    load()
+    with _lock:
+        if _autograd is None:
+            if not AUTOGRAD_PATH.is_file():
+                raise RuntimeError(
+                    f"attnres autograd extension not built: {AUTOGRAD_PATH} is missing "
+                    "(run `python fast-attnres_amd/build_native.py`)")
+            import torch  # noqa: F401  (the module links PyTorch's libraries)
+
+            spec = importlib.util.spec_from_file_location("attnres._autograd", AUTOGRAD_PATH)
+            try:
+                module = importlib.util.module_from_spec(spec)
+                spec.loader.exec_module(module)
+            except ImportError as error:
+                raise RuntimeError(f"attnres autograd extension failed to load: {error}") from error
+            _autograd = module
+    return _autograd
+
+
 def check(status: int, what: str) -> None:
     """Raise for a non-OK status, with the library's own message."""
     if status == OK:
@@ -121,4 +156,4 @@ def check(status: int, what: str) -> None:
     raise RuntimeError(f"{what}: {message} (status {status})")
 
 
-__all__ = ["LIBRARY_PATH", "SIGNATURES", "check", "load"]
+__all__ = ["AUTOGRAD_PATH", "LIBRARY_PATH", "SIGNATURES", "check", "load", "load_autograd"]

@@ -17,13 +17,14 @@ registers ``attnres::_fixed_tail_forward_with_aux`` / ``_fixed_tail_backward``
   stats, scale)`` -> ``[grad_source_0, ..., grad_source_{S-1}, grad_query]``
 
 In eager mode (not under dynamo tracing, plain tensors) ``packed_attnres``
-and ``sources_attnres`` reach the same launch functions through a direct
-``autograd.Function`` (the same saved state and gradients as the ops'
-registered autograd) instead of the op dispatcher, which costs tens of
-microseconds per read; under ``torch.compile`` they call the ops.
+and ``sources_attnres`` call the C++ autograd nodes of
+``csrc/attnres_autograd.cpp`` (``_native.load_autograd``): the same C ABI
+launches, saved state and gradients as the ops' registered autograd, without
+the op dispatcher or Python in the node's forward and backward, which cost tens
+of microseconds per read; under ``torch.compile`` they call the ops.
 
-Every output and workspace is allocated here with ``torch.empty`` on the
-caller's device; the kernels run on the current stream and the C ABI never
+Every output and workspace is allocated with ``torch.empty`` on the caller's
+device (here, or by those nodes); the kernels run on the current stream and the C ABI never
 allocates or synchronises, so the ops are safe under ``torch.compile``
 (opaque custom ops with fake kernels) and HIP/CUDA graph capture.
 
@@ -214,17 +215,6 @@ def _saved_state(tokens: int, sources: int, width: int, save: bool, device,
             floats[2 * block:].view(2, tokens))
 
 
-def _pool_addresses(pool: Tensor, tokens: int, sources: int, width: int,
-                    save: bool) -> tuple[int | None, int, int, int]:
-    """Device addresses of (out_refine or None, logit, inv_rms, stats) in a
-    pool laid out by ``_pool_layout``: the eager reads pass these to the
-    library instead of building four views (about 5 us per read)."""
-    head, block, _ = _pool_layout(tokens, sources, width, save)
-    base = pool.data_ptr()
-    logit = base + head
-    return (base if save else None), logit, logit + 4 * block, logit + 8 * block
-
-
 def _state_addresses(out_refine: Tensor, logit: Tensor, inv_rms: Tensor,
                      stats: Tensor) -> tuple[int | None, int, int, int]:
     return (_pointer(_contiguous(out_refine)), _contiguous(logit).data_ptr(), _contiguous(inv_rms).data_ptr(),
@@ -358,43 +348,6 @@ def _eager(*tensors: Tensor) -> bool:
     return not torch.compiler.is_compiling() and all(type(t) in (Tensor, torch.nn.Parameter) for t in tensors)
 
 
-class _PackedRead(torch.autograd.Function):
-    """The packed read in eager mode: the same launches, saved state and
-    gradients as the ``packed_forward`` op with its registered autograd, without
-    going through the op dispatcher (tens of microseconds per read, which bound
-    small reads).  It returns the output alone and keeps the saved state (the
-    refinement and the statistics) in one byte allocation whose addresses it
-    passes to the library: four non-differentiable outputs, or four views of
-    the pool, would cost the host about 20 us per read."""
-
-    @staticmethod
-    def forward(ctx, values: Tensor, query: Tensor, eps: float, scale: float):
-        flat = _unit_feature_stride(values)
-        dense_query = _contiguous(query)
-        sources, tokens, width = (int(size) for size in flat.shape)
-        save = saves_refinement(sources, width, dense_query.numel())
-        out = torch.empty((tokens, width), device=flat.device, dtype=_BF16)
-        pool = torch.empty((_pool_layout(tokens, sources, width, save)[2],), device=flat.device, dtype=torch.uint8)
-        _packed_forward_launch(flat, dense_query, eps, scale, out, _pool_addresses(pool, tokens, sources, width, save))
-        ctx.set_materialize_grads(False)
-        ctx.save_for_backward(values, query, pool, *((out,) if save else ()))
-        ctx.save = save
-        ctx.scale = float(scale)
-        return out
-
-    @staticmethod
-    def backward(ctx, grad_out):
-        if grad_out is None:
-            return None, None, None, None
-        values, query, pool, *out = ctx.saved_tensors
-        sources, tokens, width = (int(size) for size in values.shape)
-        state = _pool_addresses(pool, tokens, sources, width, ctx.save)
-        grad_values, grad_query = _packed_backward_launch(values, query, out[0] if out else None, grad_out, state,
-                                                          ctx.scale)
-        return (grad_values if ctx.needs_input_grad[0] else None,
-                grad_query if ctx.needs_input_grad[1] else None, None, None)
-
-
 def packed_attnres(values: Tensor, query: Tensor, eps: float, scale: float) -> Tensor:
     """Packed ``[S, ..., D]`` adapter (reference `fixed_tail.fused_attnres`,
     `fixed_tail.py:1097-1135`): flatten the batch axes to ``[S, N, D]`` as a
@@ -405,8 +358,10 @@ def packed_attnres(values: Tensor, query: Tensor, eps: float, scale: float) -> T
     if width > 1 and flat.stride(2) != 1:
         flat = flat.contiguous()
     query = _contiguous(query)
-    out = _PackedRead.apply(flat, query, eps, scale) if _eager(flat, query) else packed_forward(flat, query, eps,
-                                                                                                 scale)[0]
+    if _eager(flat, query):
+        out = _native.load_autograd().packed_read(flat, query, eps, scale)
+    else:
+        out = packed_forward(flat, query, eps, scale)[0]
     return out.reshape(values.shape[1:])
 
 
@@ -550,48 +505,13 @@ def _sources_autograd(ctx: Any, grad_out, *_aux_grads):
 sources_forward.register_autograd(_sources_autograd, setup_context=_sources_setup_context)
 
 
-class _SourcesRead(torch.autograd.Function):
-    """The source-list read in eager mode (see ``_PackedRead``); the sources
-    come after the scalars so that each list position gets its gradient."""
-
-    @staticmethod
-    def forward(ctx, query: Tensor, eps: float, scale: float, *sources: Tensor):
-        first = sources[0]
-        dense_query = _contiguous(query)
-        count, tokens, width = len(sources), _rows_of(first.shape), int(first.shape[-1])
-        save = saves_refinement(count, width, dense_query.numel())
-        out = torch.empty(first.shape, device=first.device, dtype=_BF16)
-        pool = torch.empty((_pool_layout(tokens, count, width, save)[2],), device=first.device, dtype=torch.uint8)
-        _sources_forward_launch(list(sources), dense_query, eps, scale, out,
-                                _pool_addresses(pool, tokens, count, width, save))
-        ctx.set_materialize_grads(False)
-        ctx.save_for_backward(*sources, query, pool, *((out,) if save else ()))
-        ctx.count = count
-        ctx.save = save
-        ctx.scale = float(scale)
-        return out
-
-    @staticmethod
-    def backward(ctx, grad_out):
-        count = ctx.count
-        if grad_out is None:
-            return (None, None, None, *([None] * count))
-        saved = ctx.saved_tensors
-        sources = list(saved[:count])
-        query, pool, *out = saved[count:]
-        first = sources[0]
-        state = _pool_addresses(pool, _rows_of(first.shape), count, int(first.shape[-1]), ctx.save)
-        grads = _sources_backward_launch(sources, query, out[0] if out else None, grad_out, state, ctx.scale)
-        return (grads[count] if ctx.needs_input_grad[0] else None, None, None, *grads[:count])
-
-
 def sources_attnres(sources: tuple[Tensor, ...], query: Tensor, eps: float,
                     scale: float) -> Tensor:
     """Ordered source-list adapter (reference `fixed_tail_sources.source_attnres`,
     `fixed_tail_sources.py:186-195`): the list is passed through unpacked."""
     query = _contiguous(query)
     if _eager(query, *sources):
-        return _SourcesRead.apply(query, eps, scale, *sources)
+        return _native.load_autograd().sources_read(query, eps, scale, list(sources))
     return sources_forward(list(sources), query, eps, scale)[0]
 
 

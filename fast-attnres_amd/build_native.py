@@ -8,7 +8,11 @@ library:
 * `csrc/attnres_hip.hip`: the C ABI (`include/attnres_hip.h`), host-side
   argument checks, dispatch and the dq reduction kernels;
 * `csrc/attnres_kernels.hip`, once per row geometry (lanes per token group,
-  16-byte chunks per lane) listed in GEOMETRIES.
+  16-byte chunks per lane) listed in GEOMETRIES;
+
+and, against PyTorch's headers and libraries, the eager autograd nodes
+`csrc/attnres_autograd.cpp` -> `attnres/_lib/_autograd.so` (host C++, no
+device code; linked to the library above with an `$ORIGIN` run path).
 
 Packed-FP32 VALU ops are disabled (``-target-feature -packed-fp32-ops``); the
 compiler still emits ordinary FP32 FMAs, v_dot2_f32_bf16 and the gfx950 BF16
@@ -34,6 +38,10 @@ ARCH = "gfx950"
 # in csrc/attnres_internal.h.
 GEOMETRIES = ((16, 1), (32, 1), (32, 2), (32, 4), (64, 4), (64, 8), (256, 4))
 FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+AUTOGRAD_SOURCE = CSRC / "attnres_autograd.cpp"
+AUTOGRAD_OBJECT = BUILD_DIR / "attnres_autograd.o"
+AUTOGRAD_OUTPUT = HERE / "attnres" / "_lib" / "_autograd.so"
+ROCM_INCLUDE = Path(os.environ.get("ROCM_PATH", "/opt/rocm")) / "include"
 
 
 def hipcc() -> str:
@@ -55,6 +63,31 @@ def compile_commands() -> list[tuple[list[str], Path]]:
             for source, defines, obj in units]
 
 
+def _torch_flags() -> tuple[list[str], list[str]]:
+    """Compile and link flags of a PyTorch C++ extension module named
+    `_autograd` (the same ones `torch.utils.cpp_extension` uses on ROCm)."""
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension
+
+    compile_flags = ["-O2", "-std=c++17", "-fPIC", "-DTORCH_EXTENSION_NAME=_autograd", "-DTORCH_API_INCLUDE_EXTENSION_H",
+                     f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}", "-D__HIP_PLATFORM_AMD__=1",
+                     "-DUSE_ROCM=1", f"-I{INCLUDE}", f"-I{ROCM_INCLUDE}"]
+    for path in (*cpp_extension.include_paths(), sysconfig.get_paths()["include"]):
+        compile_flags += ["-isystem", path]
+    link_flags = [f"-L{lib}" for lib in cpp_extension.library_paths()]
+    link_flags += ["-lc10", "-lc10_hip", "-ltorch_cpu", "-ltorch", "-ltorch_python"]
+    return compile_flags, link_flags
+
+
+def cxx() -> str:
+    for candidate in (os.environ.get("CXX"), shutil.which("c++"), shutil.which("g++")):
+        if candidate and Path(candidate).exists():
+            return candidate
+    raise RuntimeError("no C++ compiler found for the autograd extension")
+
+
 def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
@@ -62,7 +95,7 @@ def _run(cmd: list[str], verbose: bool) -> None:
     if result.returncode != 0:
         errors = [line for line in result.stderr.splitlines()
                   if "packed-fp32-ops" not in line and line.strip()]
-        raise RuntimeError("hipcc failed:\n" + "\n".join(errors))
+        raise RuntimeError(f"{Path(cmd[0]).name} failed:\n" + "\n".join(errors))
 
 
 def build(verbose: bool = False, jobs: int | None = None) -> Path:
@@ -70,14 +103,22 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     BUILD_DIR.mkdir(parents=True, exist_ok=True)
     OUTPUT.parent.mkdir(parents=True, exist_ok=True)
     commands = compile_commands()
-    workers = jobs or min(len(commands), os.cpu_count() or 1, 16)
+    compile_flags, link_flags = _torch_flags()
+    autograd = [cxx(), *compile_flags, "-c", str(AUTOGRAD_SOURCE), "-o", str(AUTOGRAD_OBJECT)]
+    workers = jobs or min(len(commands) + 1, os.cpu_count() or 1, 16)
     with ThreadPoolExecutor(max_workers=workers) as pool:
-        for future in [pool.submit(_run, cmd, verbose) for cmd, _ in commands]:
+        futures = [pool.submit(_run, autograd, verbose)]  # the longest unit (PyTorch headers) first
+        futures += [pool.submit(_run, cmd, verbose) for cmd, _ in commands]
+        for future in futures:
             future.result()
     temporary = OUTPUT.with_suffix(".so.tmp")
     _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC",
           *[str(obj) for _, obj in commands], "-o", str(temporary)], verbose)
     os.replace(temporary, OUTPUT)
+    temporary = AUTOGRAD_OUTPUT.with_suffix(".so.tmp")
+    _run([cxx(), "-shared", str(AUTOGRAD_OBJECT), "-o", str(temporary), f"-L{OUTPUT.parent}", "-lattnres_hip",
+          "-Wl,-rpath,$ORIGIN", *link_flags], verbose)
+    os.replace(temporary, AUTOGRAD_OUTPUT)
     return OUTPUT
 
 

@@ -262,23 +262,28 @@ def test_eager_path_choice():
 @pytest.mark.parametrize("save", [False, True])
 @pytest.mark.parametrize("tokens,sources,width", [(1, 1, 1), (7, 9, 33), (300, 25, 2048), (5, 129, 8192)])
 def test_pooled_saved_state_layout(tokens, sources, width, save):
-    """The eager read keeps its saved state in one byte pool and passes the
-    library addresses computed by ``_pool_addresses``; the pooled views of
-    ``_saved_state`` must sit at exactly those addresses, 16-byte aligned past
-    the refinement, without overlap and inside the pool."""
+    """The eager read's C++ autograd node keeps its saved state in one byte
+    pool at the offsets of its `pool_layout`; the ops' pooled views
+    (`_saved_state(pooled=True)`, used by the shared-source reads) follow the
+    Python `_pool_layout`.  Both must state the same layout: the refinement at
+    byte 0, the FP32 statistics from a 16-byte aligned offset, no overlap, all
+    inside the pool."""
     ops = _ops()
+    from attnres import _native
+
+    head, block, size = ops._pool_layout(tokens, sources, width, save)
+    assert _native.load_autograd().pool_layout(tokens, sources, width, save) == (head, block, size)
     refine, logit, inv_rms, stats = ops._saved_state(tokens, sources, width, save, "cpu", pooled=True)
     base = refine.untyped_storage().data_ptr()
-    head, block, size = ops._pool_layout(tokens, sources, width, save)
     assert refine.untyped_storage().nbytes() == size
     assert refine.shape == ((tokens if save else 0), width) and logit.shape == inv_rms.shape == (tokens, sources)
     assert stats.shape == (2, tokens)
-    pool = torch.empty(0, dtype=torch.uint8).set_(refine.untyped_storage())
-    addresses = ops._pool_addresses(pool, tokens, sources, width, save)
-    assert addresses == ((refine.data_ptr() if save else None), logit.data_ptr(), inv_rms.data_ptr(),
-                         stats.data_ptr())
+    assert (logit.data_ptr(), inv_rms.data_ptr(), stats.data_ptr()) == (base + head, base + head + 4 * block,
+                                                                        base + head + 8 * block)
+    if save:
+        assert refine.data_ptr() == base
     spans = [(t.data_ptr(), t.data_ptr() + t.numel() * t.element_size())
              for t in (refine, logit, inv_rms, stats) if t.numel()]  # an empty view reports address 0
     assert all(base <= lo <= hi <= base + size for lo, hi in spans)
     assert all(a[1] <= b[0] for a, b in zip(spans, spans[1:]))
-    assert (logit.data_ptr() - base) % 16 == 0 and head >= (tokens * width if save else 0)
+    assert head % 16 == 0 and head >= (tokens * width if save else 0)

@@ -199,10 +199,10 @@ def test_the_guard_catches_a_stacked_read():
                                    (16, 300, 4096, 1024), (25, 300, 2048, 2048)],
                          ids=["recompute", "saved", "key-resident-row", "key-resident-key", "saved-block"])
 def test_eager_function_matches_the_ops_bit_for_bit(layout, shape):
-    """In eager mode a read runs through a direct autograd.Function that keeps
-    its saved state in one pooled allocation and passes addresses to the
-    library; the registered ops (used under torch.compile) allocate each
-    saved tensor apart.  Both must launch the same kernels on the same
+    """In eager mode a read runs through the C++ autograd node of
+    csrc/attnres_autograd.cpp, which keeps its saved state in one pooled
+    allocation and passes addresses to the library; the registered ops (used
+    under torch.compile) allocate each saved tensor apart.  Both must launch the same kernels on the same
     state: out, dv and dq bit-identical, on every backward path (recompute,
     saved refinement, key-resident with a partial and a whole-row key, token
     blocks)."""
