@@ -234,3 +234,22 @@ def test_eager_function_matches_the_ops_bit_for_bit(layout, shape):
         ops = (saved[0], torch.stack(grads[:-1]), grads[-1])
     for name, a, b in zip(("out", "dv", "dq"), eager, ops):
         assert torch.equal(a, b), f"{name} differs between the eager Function and the ops"
+
+
+def test_autograd_nodes_raise_the_library_errors():
+    """The C++ nodes map a status the C ABI returns to the Python binding's
+    exception classes (ValueError for argument errors) with the library's
+    message.  `attnres` validates first, so these calls go to the nodes
+    directly, with arguments the library rejects on the host before any
+    launch: a rank above the width, and a NaN eps."""
+    from attnres import _native
+
+    nodes = _native.load_autograd()
+    values = torch.randn(3, 8, 16, device="cuda").to(torch.bfloat16)
+    query = torch.randn(17, device="cuda").to(torch.bfloat16)
+    with pytest.raises(ValueError, match="attnres packed forward"):
+        nodes.packed_read(values, query, 2**-23, 1.0)
+    with pytest.raises(ValueError, match="attnres source-list forward"):
+        nodes.sources_read(query, 2**-23, 1.0, list(values.unbind(0)))
+    with pytest.raises(ValueError, match="attnres packed forward"):
+        nodes.packed_read(values, query[:16], float("nan"), 1.0)
