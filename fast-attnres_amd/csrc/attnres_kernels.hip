@@ -1546,7 +1546,15 @@ attnres_bwd_keyres_kernel(const BwdArgs<Rows, Grads> a) {
 
     // Item ss of a token also finishes source ss of the group's previous
     // token (both have S items), so the key-part work is spread over the
-    // stream instead of bunching at each token's end.
+    // stream instead of bunching at each token's end.  4096-wide rows do that
+    // first, before the item's own dot product (the row stores and their
+    // arithmetic then overlap the wait for the item's row); 2048-wide rows
+    // after the slot's refill.  Measured on MI355X (backward us, after ->
+    // first): c3 798.8 -> 771.5; S = 9, D = 4096, R = 1024: 459.4 -> 446.0;
+    // S = 13, R = 512: 655.0 -> 647.8; but c4's shape 465.1 -> 511.0 and
+    // S = 12, D = R = 2048 300.0 -> 320.6.  Results are identical: only
+    // independent work moves, and dq accumulates in the same order.
+    constexpr bool kFinishFirst = CH == 8;
     for (int64_t ti = 0; ti < my_tokens; ++ti) {
       const bool more = ti + 1 < my_tokens;
       const int64_t next = token + groups;
@@ -1558,6 +1566,9 @@ attnres_bwd_keyres_kernel(const BwdArgs<Rows, Grads> a) {
         const int j = ss % NB;
         float p = 0.0f, dw[1] = {0.0f};
         u32x4 held[KC];
+        if constexpr (kFinishFirst) {
+          if (ss < S && prev >= 0) finish(ss);  // uniform
+        }
         if (ss < S) {
           {
             float dw1 = 0.0f;
@@ -1601,7 +1612,9 @@ attnres_bwd_keyres_kernel(const BwdArgs<Rows, Grads> a) {
           load_item(j, next, sn - Sp, more && sn - Sp < S);
         }
         if (ss < S) {
-          if (prev >= 0) finish(ss);  // uniform
+          if constexpr (!kFinishFirst) {
+            if (prev >= 0) finish(ss);  // uniform
+          }
 #pragma unroll
           for (int c = 0; c < KC; ++c) key[ss][c] = held[c];
           kp[ss] = p;
