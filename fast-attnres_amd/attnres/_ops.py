@@ -352,17 +352,16 @@ def packed_attnres(values: Tensor, query: Tensor, eps: float, scale: float) -> T
     """Packed ``[S, ..., D]`` adapter (reference `fixed_tail.fused_attnres`,
     `fixed_tail.py:1097-1135`): flatten the batch axes to ``[S, N, D]`` as a
     view when the layout allows it (a copy only otherwise), call the op and
-    restore the batch shape."""
+    restore the batch shape.  The eager node does the flattening inside, so
+    autograd records no view nodes around it."""
+    query = _contiguous(query)
+    if _eager(values, query):
+        return _native.load_autograd().packed_read(values, query, eps, scale)
     sources, width = int(values.shape[0]), int(values.shape[-1])
     flat = values.reshape(sources, -1, width)
     if width > 1 and flat.stride(2) != 1:
         flat = flat.contiguous()
-    query = _contiguous(query)
-    if _eager(flat, query):
-        out = _native.load_autograd().packed_read(flat, query, eps, scale)
-    else:
-        out = packed_forward(flat, query, eps, scale)[0]
-    return out.reshape(values.shape[1:])
+    return packed_forward(flat, query, eps, scale)[0].reshape(values.shape[1:])
 
 
 # -------------------------------------------------------------------- list

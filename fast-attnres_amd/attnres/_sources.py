@@ -20,7 +20,7 @@ _MAX_WIDTH = 8192
 
 def check_scalar(value, name: str, *, positive: bool = False) -> float:
     """Accept real Python/NumPy scalars only (not bool, str or tensors)."""
-    if isinstance(value, bool) or not isinstance(value, Real):
+    if type(value) is not float and (isinstance(value, bool) or not isinstance(value, Real)):
         raise TypeError(f"{name} must be a real scalar")
     number = float(value)
     if not math.isfinite(number):
@@ -38,12 +38,13 @@ def check_packed(values: torch.Tensor, query, eps, scale) -> tuple[float, float]
     """
     if not isinstance(query, torch.Tensor):
         raise TypeError("query must be a tensor")
-    if values.ndim < 2 or query.ndim != 1:
+    shape = values.shape
+    if len(shape) < 2 or query.ndim != 1:
         raise ValueError("expected values [S,...,D] and query [R]")
-    if not 1 <= values.shape[0] <= _MAX_SOURCES or not 1 <= values.shape[-1] <= _MAX_WIDTH:
+    if not 1 <= shape[0] <= _MAX_SOURCES or not 1 <= shape[-1] <= _MAX_WIDTH:
         raise ValueError(
             f"supported envelope is 1<=S<={_MAX_SOURCES} and 1<=D<={_MAX_WIDTH}")
-    if any(size < 1 for size in values.shape) or not 1 <= query.numel() <= values.shape[-1]:
+    if min(shape) < 1 or not 1 <= query.numel() <= shape[-1]:
         raise ValueError("dimensions must be positive and 1<=R<=D")
     if values.dtype != torch.bfloat16:
         raise TypeError("values must use BF16 storage")

@@ -236,6 +236,48 @@ def test_eager_function_matches_the_ops_bit_for_bit(layout, shape):
         assert torch.equal(a, b), f"{name} differs between the eager Function and the ops"
 
 
+@pytest.mark.parametrize("layout", ["batch-axes", "uncollapsible", "feature-strided", "no-batch"])
+@pytest.mark.parametrize("sources", [5, 9])
+def test_eager_node_flattens_batch_axes_itself(layout, sources):
+    """The eager node takes packed values [S, ..., D] as they come and
+    flattens the batch axes inside its forward (a view where they collapse to
+    one row stride, a copy otherwise or when a row is not unit-stride), so
+    the graph holds the node alone: no view node between it and the leaf,
+    the output in the batch shape, the value gradient in the shape of values.
+    Results are those of the ops on the flattened contiguous values,
+    bit for bit, on the recompute (S = 5) and saved (S = 9) paths."""
+    torch.manual_seed(11)
+    width, rank = 1024, 256
+    print(f"eager node batch axes {layout} S={sources}", flush=True)
+    if layout == "batch-axes":
+        leaf = torch.randn(sources, 3, 70, width, device="cuda").to(torch.bfloat16)
+    elif layout == "uncollapsible":  # [S, 70, 3, D] viewed as [S, 3, 70, D]: no single row stride
+        leaf = torch.randn(sources, 70, 3, width, device="cuda").to(torch.bfloat16).transpose(1, 2)
+    elif layout == "feature-strided":  # [S, D, 210] transposed: rows are not unit-stride
+        leaf = torch.randn(sources, width, 210, device="cuda").to(torch.bfloat16).transpose(1, 2)
+    else:  # [S, D]: one token
+        leaf = torch.randn(sources, width, device="cuda").to(torch.bfloat16)
+    leaf.requires_grad_()
+    query = (torch.randn(rank, device="cuda") / rank ** 0.5).to(torch.bfloat16).requires_grad_()
+    upstream = torch.randn(leaf.shape[1:], device="cuda").to(torch.bfloat16)
+    out = attnres(leaf, query)
+    assert out.shape == leaf.shape[1:]
+    assert all(type(fn).__name__ in ("AccumulateGrad", "NoneType") for fn, _ in out.grad_fn.next_functions), \
+        f"expected the node alone, found {out.grad_fn.next_functions}"
+    dv, dq = torch.autograd.grad(out, (leaf, query), upstream)
+    assert dv.shape == leaf.shape
+
+    from attnres import _ops  # noqa: F401  (registers the ops)
+    flat = leaf.detach().reshape(sources, -1, width).contiguous()
+    q = query.detach()
+    saved = torch.ops.attnres_hip.packed_forward(flat, q, 2**-23, 1.0)
+    grads = torch.ops.attnres_hip.packed_backward(flat, q, saved[0], saved[1], upstream.reshape(-1, width),
+                                                  *saved[2:], 1.0)
+    assert torch.equal(out.reshape(-1, width), saved[0]), "out differs from the ops"
+    assert torch.equal(dv.reshape(sources, -1, width), grads[0]), "dv differs from the ops"
+    assert torch.equal(dq, grads[1]), "dq differs from the ops"
+
+
 def test_autograd_nodes_raise_the_library_errors():
     """The C++ nodes map a status the C ABI returns to the Python binding's
     exception classes (ValueError for argument errors) with the library's
