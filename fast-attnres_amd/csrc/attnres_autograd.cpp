@@ -12,7 +12,7 @@
 // autograd.Function, with torch's own floor for a trivial graph at 62 us.
 // The packed node also flattens the batch axes itself (two view nodes less
 // in the graph): c1's [8, 2, 512, 1024] read 37 us on a box whose floor is
-// 29.5 us.
+// 29.5 us.  A read that needs no gradient skips the nodes (below).
 //
 // Saved state: the refinement bytes (when the read saves them) and the FP32
 // statistics live in one byte allocation whose addresses are passed to the
@@ -272,11 +272,67 @@ struct SourcesRead : public torch::autograd::Function<SourcesRead> {
   }
 };
 
+// ------------------------------------------------------ no gradient needed
+
+// Grad mode off (torch.no_grad, inference_mode) or no input requiring grad:
+// no node, no saved state and no refinement bytes (the forward takes
+// out_refine = NULL for any S); the statistics the kernels write go to a
+// scratch allocation freed on return.  out is the same, bit for bit.
+bool needs_grad(const Tensor& query, at::TensorList sources) {
+  if (!at::GradMode::is_enabled()) return false;
+  if (query.requires_grad()) return true;
+  for (const Tensor& source : sources) {
+    if (source.requires_grad()) return true;
+  }
+  return false;
+}
+
+Tensor statistics_scratch(int64_t tokens, int64_t sources, const Tensor& like, StatePointers* state) {
+  const PoolLayout layout = pool_layout(tokens, sources, 0, false);
+  Tensor pool = torch::empty({layout.size}, like.options().dtype(torch::kUInt8));
+  *state = pool_pointers(pool, layout, false);
+  return pool;
+}
+
+Tensor packed_forward_only(const Tensor& values, const Tensor& query, double eps, double scale) {
+  const int64_t S = values.size(0), D = values.size(-1), R = query.numel();
+  Tensor rows = values.dim() == 3 ? values : values.reshape({S, -1, D});
+  if (D > 1 && rows.stride(2) != 1) rows = rows.contiguous();
+  const int64_t N = rows.size(1);
+  const c10::DeviceGuard guard(values.device());
+  Tensor out = bf16_empty(values.sizes().slice(1), values);
+  StatePointers state{};
+  const Tensor scratch = statistics_scratch(N, S, values, &state);
+  check(attnres_hip_packed_forward(rows.data_ptr(), rows.stride(0), rows.stride(1), S, N, D, query.data_ptr(), R,
+                                   static_cast<float>(eps), static_cast<float>(scale), out.data_ptr(), nullptr,
+                                   state.logit, state.inv_rms, state.stats, current_stream(values)),
+        "attnres packed forward");
+  return out;
+}
+
+Tensor sources_forward_only(const Tensor& query, double eps, double scale, at::TensorList sources) {
+  const Tensor& first = sources[0];
+  const int64_t S = static_cast<int64_t>(sources.size()), N = rows_of(first), D = first.size(-1);
+  const c10::DeviceGuard guard(first.device());
+  const SourceTable table = source_table(sources);
+  Tensor out = bf16_empty(first.sizes(), first);
+  StatePointers state{};
+  const Tensor scratch = statistics_scratch(N, S, first, &state);
+  check(attnres_hip_sources_forward(table.rows.data(), table.strides.data(), S, N, D, query.data_ptr(),
+                                    query.numel(), static_cast<float>(eps), static_cast<float>(scale),
+                                    out.data_ptr(), nullptr, state.logit, state.inv_rms, state.stats,
+                                    current_stream(first)),
+        "attnres source-list forward");
+  return out;
+}
+
 Tensor packed_read(const Tensor& values, const Tensor& query, double eps, double scale) {
+  if (!needs_grad(query, values)) return packed_forward_only(values, query, eps, scale);
   return PackedRead::apply(values, query, eps, scale);
 }
 
 Tensor sources_read(const Tensor& query, double eps, double scale, const std::vector<Tensor>& sources) {
+  if (!needs_grad(query, sources)) return sources_forward_only(query, eps, scale, sources);
   return SourcesRead::apply(query, eps, scale, at::TensorList(sources));
 }
 

@@ -278,6 +278,48 @@ def test_eager_node_flattens_batch_axes_itself(layout, sources):
     assert torch.equal(dq, grads[1]), "dq differs from the ops"
 
 
+@pytest.mark.parametrize("layout", ["packed", "list"])
+@pytest.mark.parametrize("sources", [5, 9, 25])
+def test_reads_without_gradients_store_no_saved_state(layout, sources):
+    """With grad mode off (torch.no_grad, torch.inference_mode) or no input
+    requiring grad, an eager read runs the forward alone: no autograd node,
+    no refinement bytes and no saved state held after the call, and the
+    output is the training forward's, bit for bit (the recompute, saved and
+    token-block paths)."""
+    torch.manual_seed(5)
+    width, tokens = 2048, 300
+    print(f"no-grad read {layout} S={sources}", flush=True)
+    values = torch.randn(sources, 3, tokens // 3, width, device="cuda").to(torch.bfloat16)
+    query = (torch.randn(width, device="cuda") / width ** 0.5).to(torch.bfloat16)
+
+    def call(v, q):
+        return attnres(v if layout == "packed" else list(v.unbind(0)), q)
+
+    leaf = values.clone().requires_grad_()
+    trained = call(leaf, query)
+    assert trained.grad_fn is not None
+    expected = trained.detach().clone()
+    del trained, leaf
+    torch.cuda.synchronize()
+    out_bytes = expected.numel() * expected.element_size()
+    for mode in ("no_grad", "inference_mode", "no input requires grad"):
+        before = torch.cuda.memory_allocated()
+        if mode == "no_grad":
+            with torch.no_grad():
+                out = call(values.clone().requires_grad_(), query)
+        elif mode == "inference_mode":
+            with torch.inference_mode():
+                out = call(values, query)
+        else:
+            out = call(values, query)
+        torch.cuda.synchronize()
+        assert out.grad_fn is None, mode
+        assert torch.equal(out, expected), f"{mode}: the output differs from the training forward's"
+        held = torch.cuda.memory_allocated() - before
+        assert held <= out_bytes + 512, f"{mode}: {held} bytes held after the call, the output is {out_bytes}"
+        del out
+
+
 def test_autograd_nodes_raise_the_library_errors():
     """The C++ nodes map a status the C ABI returns to the Python binding's
     exception classes (ValueError for argument errors) with the library's
