@@ -16,6 +16,10 @@ registers ``attnres::_fixed_tail_forward_with_aux`` / ``_fixed_tail_backward``
 * ``sources_backward(sources, query, out, out_refine, grad_out, logit, inv_rms,
   stats, scale)`` -> ``[grad_source_0, ..., grad_source_{S-1}, grad_query]``
 
+and two more for reads that need no gradient (grad mode off, or no input
+requiring grad), which return the output alone and store no refinement or
+saved state: ``packed_forward_out`` and ``sources_forward_out``.
+
 In eager mode (not under dynamo tracing, plain tensors) ``packed_attnres``
 and ``sources_attnres`` call the C++ autograd nodes of
 ``csrc/attnres_autograd.cpp`` (``_native.load_autograd``): the same C ABI
@@ -268,6 +272,21 @@ def _packed_forward_fake(values, query, eps, scale):
             values.new_empty((2, tokens), dtype=_F32))
 
 
+@torch.library.custom_op("attnres_hip::packed_forward_out", mutates_args=(),
+                         device_types="cuda", tags=_OP_TAGS)
+def packed_forward_out(values: Tensor, query: Tensor, eps: float, scale: float) -> Tensor:
+    """The packed forward of a read that needs no gradient: the output alone.
+    No refinement bytes are stored (the C ABI takes ``out_refine = NULL`` at
+    any S); the statistics the kernels write live in scratch freed on
+    return.  The output is ``packed_forward``'s, bit for bit."""
+    return packed_forward_impl(values, query, eps, scale, False, pooled=True)[0]
+
+
+@packed_forward_out.register_fake
+def _packed_forward_out_fake(values, query, eps, scale):
+    return values.new_empty((values.shape[1], values.shape[2]))
+
+
 def _packed_backward_launch(values: Tensor, query: Tensor, out: Tensor | None, grad_out: Tensor,
                             state: tuple[int | None, int, int, int], scale: float) -> tuple[Tensor, Tensor]:
     """``attnres_hip_packed_backward`` with the saved state at ``state``
@@ -342,6 +361,12 @@ def _packed_autograd(ctx: Any, grad_out, *_aux_grads):
 packed_forward.register_autograd(_packed_autograd, setup_context=_packed_setup_context)
 
 
+def _needs_grad(query: Tensor, *sources: Tensor) -> bool:
+    """Whether autograd will want gradients of this read (grad mode on and an
+    input that requires grad); traced as a guarded constant under dynamo."""
+    return torch.is_grad_enabled() and (query.requires_grad or any(s.requires_grad for s in sources))
+
+
 def _eager(*tensors: Tensor) -> bool:
     """An eager call: not under dynamo tracing, and only plain tensors or
     parameters (no fake or functional tensors of a compiler's tracing)."""
@@ -361,6 +386,8 @@ def packed_attnres(values: Tensor, query: Tensor, eps: float, scale: float) -> T
     flat = values.reshape(sources, -1, width)
     if width > 1 and flat.stride(2) != 1:
         flat = flat.contiguous()
+    if not _needs_grad(query, values):
+        return packed_forward_out(flat, query, eps, scale).reshape(values.shape[1:])
     return packed_forward(flat, query, eps, scale)[0].reshape(values.shape[1:])
 
 
@@ -413,6 +440,19 @@ def sources_forward(sources: list[Tensor], query: Tensor, eps: float,
                     scale: float) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     return sources_forward_impl(sources, query, eps, scale,
                                 saves_refinement(len(sources), int(sources[0].shape[-1]), query.numel()))
+
+
+@torch.library.custom_op("attnres_hip::sources_forward_out", mutates_args=(),
+                         device_types="cuda", tags=_OP_TAGS)
+def sources_forward_out(sources: list[Tensor], query: Tensor, eps: float, scale: float) -> Tensor:
+    """The source-list forward of a read that needs no gradient (as
+    ``packed_forward_out``)."""
+    return sources_forward_impl(sources, query, eps, scale, False, pooled=True)[0]
+
+
+@sources_forward_out.register_fake
+def _sources_forward_out_fake(sources, query, eps, scale):
+    return sources[0].new_empty(sources[0].shape)
 
 
 @sources_forward.register_fake
@@ -511,11 +551,13 @@ def sources_attnres(sources: tuple[Tensor, ...], query: Tensor, eps: float,
     query = _contiguous(query)
     if _eager(query, *sources):
         return _native.load_autograd().sources_read(query, eps, scale, list(sources))
+    if not _needs_grad(query, *sources):
+        return sources_forward_out(list(sources), query, eps, scale)
     return sources_forward(list(sources), query, eps, scale)[0]
 
 
 __all__ = [
     "KEYRES_FULL_MAX_SOURCES", "KEYRES_MAX_SOURCES", "RECOMPUTE_MAX_SOURCES", "keyres_key_chunks", "packed_attnres", "packed_backward", "packed_backward_impl", "packed_forward",
-    "packed_forward_impl", "prepare_rows", "row_stride", "saves_refinement", "sources_attnres", "sources_backward",
-    "sources_backward_impl", "sources_forward", "sources_forward_impl",
+    "packed_forward_impl", "packed_forward_out", "prepare_rows", "row_stride", "saves_refinement", "sources_attnres",
+    "sources_backward", "sources_backward_impl", "sources_forward", "sources_forward_impl", "sources_forward_out",
 ]

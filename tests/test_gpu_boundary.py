@@ -12,6 +12,11 @@
   ``aten.stack`` / ``aten.cat`` whose inputs are the read's sources watches
   an eager and a compiled list read, forward and backward.  A negative control
   shows the guard catches the oracle's own stack.
+* The eager C++ nodes against the ops, bit for bit, on every backward path;
+  the packed node flattening batch axes itself (no view nodes).
+* Reads without gradients (no_grad, inference_mode, no input requiring
+  grad), eager and compiled: the forward alone, no saved state, the training
+  forward's output bit for bit.
 """
 
 from __future__ import annotations
@@ -318,6 +323,46 @@ def test_reads_without_gradients_store_no_saved_state(layout, sources):
         held = torch.cuda.memory_allocated() - before
         assert held <= out_bytes + 512, f"{mode}: {held} bytes held after the call, the output is {out_bytes}"
         del out
+
+
+@pytest.mark.parametrize("layout", ["packed", "list"])
+def test_compiled_reads_without_gradients_call_the_forward_alone(layout, monkeypatch):
+    """Under torch.compile a read that needs no gradient calls
+    ``packed_forward_out`` / ``sources_forward_out`` (the output alone, no
+    refinement bytes or saved state) instead of the saving forward op, and
+    its output is the eager training forward's, bit for bit.  Both ops launch
+    through ``*_forward_impl``; the calls it records name the op that ran
+    (``save`` False and the state pooled for the forward alone)."""
+    from attnres import _ops
+
+    torch.manual_seed(6)
+    sources, width = 25, 2048
+    print(f"compiled no-grad read {layout}", flush=True)
+    values = torch.randn(sources, 256, width, device="cuda").to(torch.bfloat16)
+    query = (torch.randn(width, device="cuda") / width ** 0.5).to(torch.bfloat16)
+
+    def read(v, q):
+        return attnres(v if layout == "packed" else list(v.unbind(0)), q)
+
+    expected = read(values.clone().requires_grad_(), query).detach()
+    name = "packed_forward_impl" if layout == "packed" else "sources_forward_impl"
+    impl = getattr(_ops, name)
+    calls = []
+
+    def recording(*args, **kwargs):
+        calls.append((args[4], kwargs.get("pooled", args[5] if len(args) > 5 else False)))
+        return impl(*args, **kwargs)
+
+    monkeypatch.setattr(_ops, name, recording)
+    torch._dynamo.reset()
+    compiled = torch.compile(read, fullgraph=True, dynamic=False)
+    with torch.no_grad():
+        compiled(values, query)  # compile
+        calls.clear()
+        out = compiled(values, query)
+    assert calls == [(False, True)], f"expected the forward alone, got (save, pooled) calls {calls}"
+    assert torch.equal(out, expected), "the compiled no-grad output differs from the training forward's"
+    torch._dynamo.reset()
 
 
 def test_autograd_nodes_raise_the_library_errors():
