@@ -1008,6 +1008,26 @@ def main(argv=None) -> int:
     bwd_ms = [e[1].elapsed_time(e[2]) for e in events]
     cold_ms = _cold_inputs_ms(cfg, device, values, query, grad_out, args.steps)
 
+    # Serving: forward-only loops (each forward follows another forward of the same
+    # values), under torch.no_grad (the forward alone: no refinement bytes or saved
+    # state) and with grad enabled (the training forward, saving state for a
+    # backward), so the two are timed alike.
+    def forward_loop(grad: bool) -> float:
+        with torch.set_grad_enabled(grad):
+            for _ in range(args.warmup):
+                attnres(values, query)
+            torch.cuda.synchronize()
+            begin, end = _event(), _event()
+            begin.record()
+            for _ in range(args.steps):
+                attnres(values, query)
+            end.record()
+            torch.cuda.synchronize()
+        return begin.elapsed_time(end) / args.steps
+
+    inference_ms = forward_loop(False)
+    saving_forward_ms = forward_loop(True)
+
     ms_per_step = total_ms / args.steps
     fwd_avg = statistics.fmean(fwd_ms)
     bwd_avg = statistics.fmean(bwd_ms)
@@ -1055,6 +1075,13 @@ def main(argv=None) -> int:
                     "pct_of_peak": round(100 * fwd_tbs / HBM_PEAK_TBS, 2)},
         "backward": {"us": round(bwd_avg * 1e3, 2), "bytes": bwd_bytes, "TB/s": round(bwd_tbs, 4),
                      "pct_of_peak": round(100 * bwd_tbs / HBM_PEAK_TBS, 2)},
+        "inference_forward": {
+            "us": round(inference_ms * 1e3, 2),
+            "TB/s": round(fwd_bytes / (inference_ms * 1e-3) / 1e12, 4),
+            "pct_of_peak": round(100 * fwd_bytes / (inference_ms * 1e-3) / 1e12 / HBM_PEAK_TBS, 2),
+            "saving_forward_us": round(saving_forward_ms * 1e3, 2),
+            "what": "K forwards in a row under torch.no_grad (no autograd node, refinement bytes or saved state); "
+                    "saving_forward_us: the same loop with grad enabled (the training forward)"},
         "roofline": {"bound": "hbm",
                      "kernel": f"backward op: {backward_kernel(sources, width, cfg['rank'])} + attnres_dq_reduce_kernel",
                      "achieved": round(bwd_tbs * 1e3, 1), "peak": HBM_PEAK_TBS * 1e3,
