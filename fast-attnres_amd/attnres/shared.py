@@ -154,6 +154,9 @@ class SharedSources:
         """``attnres(sources, query, eps=eps, scale=scale)`` with the source
         gradients summed in the kernels across this bank's reads."""
         _, eps_value, scale_value = check_sources(self.sources, query, eps, scale)
+        if not _needs_gradients(query, self._token):  # the forward alone: nothing saved
+            return sources_forward_impl(list(self.sources), _contiguous(query), eps_value, scale_value, False,
+                                        pooled=True)[0]
         return _Read.apply(self._state, self._token, query, eps_value, scale_value)
 
 
@@ -473,7 +476,23 @@ class SourceBank:
         # the slots were checked at their push: BF16 rows [..., D] on one device
         state = self._state
         eps_value, scale_value = check_query(query, state._width, state._device, eps, scale)
+        if not _needs_gradients(query, self._token):  # the forward alone: nothing saved
+            query = _contiguous(query)
+            if state._prefix(tuple(slots)):
+                out = packed_forward_impl(state._flat[:len(slots)], query, eps_value, scale_value, False, pooled=True)[0]
+            else:
+                out = sources_forward_impl(state._sources(tuple(slots)), query, eps_value, scale_value, False,
+                                           pooled=True)[0]
+            return out.reshape(state._values.shape[1:])
         return _BankRead.apply(self._state, tuple(slots), query, eps_value, scale_value, self._token)
+
+
+def _needs_gradients(query: Tensor, token: Tensor | None) -> bool:
+    """Whether autograd will want this read's gradients: grad mode on and the
+    query or the sources (through the container's token) requiring grad.
+    Otherwise a read runs the forward alone, with no refinement bytes or
+    saved state, and the same output bits."""
+    return torch.is_grad_enabled() and (query.requires_grad or (token is not None and token.requires_grad))
 
 
 def _token_input_grad(ctx, index: int) -> Tensor | None:

@@ -532,3 +532,38 @@ def test_source_bank_tail_reads_within_float64_bound(gradients):
     for leaf in range(6):
         bound = accumulated_bound(contributions[leaf], allowances[leaf], roundings=0)
         check_accumulated(results[leaf], sum(contributions[leaf]), bound, f"leaf{leaf}")
+
+
+@pytest.mark.parametrize("kind", ["shared", "bank", "bank-tail"])
+def test_reads_without_gradients_run_the_forward_alone(kind):
+    """A SharedSources or SourceBank read that needs no gradient (grad mode
+    off, or neither the query nor the sources requiring grad) runs the
+    forward alone: no autograd node, no refinement bytes or saved state, and
+    the output of the same read with gradients, bit for bit."""
+    from attnres import SourceBank
+
+    torch.manual_seed(13)
+    print(f"no-grad {kind} read", flush=True)
+    sources = [(torch.randn(2, 150, 1024, device="cuda") * (0.5 + s / 4)).to(torch.bfloat16) for s in range(9)]
+    query = (torch.randn(1024, device="cuda") / 32).to(torch.bfloat16)
+
+    def read(leaves, q):
+        if kind == "shared":
+            return SharedSources(leaves).read(q)
+        bank = SourceBank(len(leaves))
+        for leaf in leaves:
+            bank.push(leaf)
+        return bank.read(q, count=4, tail=7) if kind == "bank-tail" else bank.read(q)
+
+    trained = read([s.clone().requires_grad_() for s in sources], query.clone().requires_grad_())
+    assert trained.grad_fn is not None
+    expected = trained.detach().clone()
+    del trained
+    for mode in ("no_grad", "no input requires grad"):
+        if mode == "no_grad":
+            with torch.no_grad():
+                out = read([s.clone().requires_grad_() for s in sources], query.clone().requires_grad_())
+        else:
+            out = read(sources, query)
+        assert out.grad_fn is None, mode
+        assert torch.equal(out, expected), f"{mode}: the output differs from the read with gradients"
