@@ -8,6 +8,7 @@ agree to the rounding of a BF16 sum (the bank adds each read's FP32 dv to the
 running BF16 sum; autograd adds BF16-rounded dv) and match the oracle's
 summed gradients to the BF16 gate.  The shapes follow config c4 at a reduced
 token count (9 separately allocated sources, 3 reads) plus a masked width.
+Reads that need no gradient run the forward alone, with the same output bits.
 """
 
 from __future__ import annotations
