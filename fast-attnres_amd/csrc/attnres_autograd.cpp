@@ -139,19 +139,27 @@ SourceTable source_table(at::TensorList sources) {
 
 int64_t rows_of(const Tensor& tensor) { return tensor.dim() > 1 ? tensor.numel() / tensor.size(-1) : 1; }
 
+// Packed values [S, ..., D] as rows [S, N, D]: a view where the batch axes
+// collapse to one row stride (as torch's reshape does), a copy otherwise, and
+// a copy too when a row is not unit-stride.  Called inside a node's forward
+// (or with no node at all), so autograd records no view nodes for it.
+Tensor flat_rows(const Tensor& values) {
+  const int64_t S = values.size(0), D = values.size(-1);
+  Tensor rows = values.dim() == 3 ? values : values.reshape({S, -1, D});
+  if (D > 1 && rows.stride(2) != 1) rows = rows.contiguous();
+  return rows;
+}
+
 // ------------------------------------------------------------------ packed
 
 struct PackedRead : public torch::autograd::Function<PackedRead> {
   // values [S, ..., D] (checked by the Python caller), query [R] contiguous.
-  // The batch axes flatten to N rows here, as torch's reshape does (a view
-  // when they collapse to one row stride, a copy otherwise; a copy too when a
-  // row is not unit-stride), so autograd records no view nodes around the
-  // read: the output has the batch shape [..., D] and the value gradient the
-  // shape of values.
+  // The batch axes flatten to N rows here (flat_rows), so autograd records no
+  // view nodes around the read: the output has the batch shape [..., D] and
+  // the value gradient the shape of values.
   static Tensor forward(AutogradContext* ctx, const Tensor& values, const Tensor& query, double eps, double scale) {
     const int64_t S = values.size(0), D = values.size(-1), R = query.numel();
-    Tensor rows = values.dim() == 3 ? values : values.reshape({S, -1, D});
-    if (D > 1 && rows.stride(2) != 1) rows = rows.contiguous();
+    const Tensor rows = flat_rows(values);
     const int64_t N = rows.size(1);
     const bool save = attnres_hip_saves_refinement_for(S, D, R) != 0;
     const c10::DeviceGuard guard(values.device());
@@ -296,8 +304,7 @@ Tensor statistics_scratch(int64_t tokens, int64_t sources, const Tensor& like, S
 
 Tensor packed_forward_only(const Tensor& values, const Tensor& query, double eps, double scale) {
   const int64_t S = values.size(0), D = values.size(-1), R = query.numel();
-  Tensor rows = values.dim() == 3 ? values : values.reshape({S, -1, D});
-  if (D > 1 && rows.stride(2) != 1) rows = rows.contiguous();
+  const Tensor rows = flat_rows(values);
   const int64_t N = rows.size(1);
   const c10::DeviceGuard guard(values.device());
   Tensor out = bf16_empty(values.sizes().slice(1), values);
