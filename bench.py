@@ -839,6 +839,27 @@ def run_model(cfg: dict, steps: int, warmup: int, variant: str = "both", autocas
         torch.cuda.synchronize()
         return start.elapsed_time(stop) / steps, float(loss)
 
+    def time_inference(source_bank):
+        # serving: the model's forward (logits) under torch.no_grad, so every read runs
+        # the forward alone (no autograd nodes, refinement bytes or saved state)
+        torch.manual_seed(0)
+        model = make_model(config, backend="kernel", source_bank=source_bank).cuda()
+
+        def forward():
+            with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+                return model(tokens)
+
+        for _ in range(warmup):
+            forward()
+        torch.cuda.synchronize()
+        start, stop = _event(), _event()
+        start.record()
+        for _ in range(steps):
+            forward()
+        stop.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) / steps
+
     graph_ms, graph_loss = time_graph() if variant == "graph" else (None, None)
     ms, loss = time_steps(False) if variant in ("both", "plain") else (None, None)
     bank_ms, bank_loss = time_steps(True) if variant in ("both", "bank") else (None, None)
@@ -846,6 +867,8 @@ def run_model(cfg: dict, steps: int, warmup: int, variant: str = "both", autocas
     comp_ms, comp_loss = time_steps(False, compiled=True) if variant == "compiled" else (None, None)
     bc_ms, bc_loss = (time_steps(True, compile_layers=True) if variant in ("both", "bank_compiled")
                       else (None, None))
+    inference_ms = time_inference(False) if variant == "both" else None
+    inference_bank_ms = time_inference(True) if variant == "both" else None
 
     def rate(t):
         return None if t is None else round(n_tokens / (t * 1e-3), 1)
@@ -890,6 +913,10 @@ def run_model(cfg: dict, steps: int, warmup: int, variant: str = "both", autocas
         "compiled": {"ms_per_step": rounded(comp_ms, 3), "tokens_per_s": rate(comp_ms), "loss": rounded(comp_loss, 4)},
         # --model-variant graph: the whole step captured in one HIP graph (BF16 autocast)
         "graph": {"ms_per_step": rounded(graph_ms, 3), "tokens_per_s": rate(graph_ms), "loss": rounded(graph_loss, 4)},
+        # serving: the model's forward alone under torch.no_grad, plain and with the source bank
+        "inference": {"ms_per_forward": rounded(inference_ms, 3), "tokens_per_s": rate(inference_ms),
+                      "source_bank_ms_per_forward": rounded(inference_bank_ms, 3),
+                      "source_bank_tokens_per_s": rate(inference_bank_ms)},
         "roofline": None,
         "cpu_baseline": None,
     }
