@@ -13,7 +13,8 @@
   an eager and a compiled list read, forward and backward.  A negative control
   shows the guard catches the oracle's own stack.
 * The eager C++ nodes against the ops, bit for bit, on every backward path;
-  the packed node flattening batch axes itself (no view nodes).
+  the packed node flattening batch axes itself (no view nodes), on fixed and
+  seeded random layouts.
 * Reads without gradients (no_grad, inference_mode, no input requiring
   grad), eager and compiled: the forward alone, no saved state, the training
   forward's output bit for bit.
@@ -382,3 +383,61 @@ def test_autograd_nodes_raise_the_library_errors():
         nodes.sources_read(query, 2**-23, 1.0, list(values.unbind(0)))
     with pytest.raises(ValueError, match="attnres packed forward"):
         nodes.packed_read(values, query[:16], float("nan"), 1.0)
+
+
+def _random_layout_cases(count=24, seed=20261203):
+    """Seeded (S, batch shape, D, R, layout) draws over the envelope: one to
+    three batch axes, widths from 8 to 4096 (aligned or not), any rank, and
+    three memory layouts of the packed tensor."""
+    import random
+
+    rng = random.Random(seed)
+    cases = []
+    for _ in range(count):
+        sources = rng.choice([1, 2, 5, 7, 9, 13, 16, 25, 30])
+        width = rng.choice([8, 40, 200, 512, 1000, 1024, 2048, 3000, 4096])
+        rank = rng.choice([width, max(1, width // 4), rng.randint(1, width)])
+        batch = tuple(rng.randint(1, 40) for _ in range(rng.randint(1, 3)))
+        layout = rng.choice(["contiguous", "batch-transposed", "feature-strided"])
+        cases.append((sources, batch, width, rank, layout))
+    return cases
+
+
+@pytest.mark.parametrize("sources,batch,width,rank,layout", _random_layout_cases())
+def test_eager_node_random_layouts_match_the_ops(sources, batch, width, rank, layout):
+    """Random packed layouts through the eager node against the ops on the
+    flattened contiguous values, bit for bit (out, dv, dq), and the forward
+    without gradients against the training forward."""
+    torch.manual_seed(sources * 1000 + width + rank)
+    print(f"random layout S={sources} batch={batch} D={width} R={rank} {layout}", flush=True)
+    if layout == "contiguous":
+        base = torch.randn(sources, *batch, width, device="cuda").to(torch.bfloat16)
+    elif layout == "batch-transposed" and len(batch) >= 2:
+        base = torch.randn(sources, *batch[::-1], width, device="cuda").to(torch.bfloat16)
+        base = base.permute(0, *range(len(batch), 0, -1), len(batch) + 1)
+    elif layout == "feature-strided":
+        base = torch.randn(sources, width, *batch, device="cuda").to(torch.bfloat16)
+        base = base.permute(0, *range(2, len(batch) + 2), 1)
+    else:  # a transposed batch needs two batch axes: a strided row selection instead
+        base = torch.randn(sources, *batch[:-1], 2 * batch[-1], width, device="cuda").to(torch.bfloat16)
+        base = base[..., ::2, :]
+    assert base.shape == (sources, *batch, width)
+    leaf = base.clone(memory_format=torch.preserve_format).requires_grad_() if layout == "contiguous" \
+        else base.detach().requires_grad_()
+    query = (torch.randn(rank, device="cuda") / rank ** 0.5).to(torch.bfloat16).requires_grad_()
+    upstream = torch.randn(*batch, width, device="cuda").to(torch.bfloat16)
+    out = attnres(leaf, query)
+    dv, dq = torch.autograd.grad(out, (leaf, query), upstream)
+    assert out.shape == (*batch, width) and dv.shape == leaf.shape
+
+    from attnres import _ops  # noqa: F401  (registers the ops)
+    flat = leaf.detach().reshape(sources, -1, width).contiguous()
+    q = query.detach()
+    saved = torch.ops.attnres_hip.packed_forward(flat, q, 2**-23, 1.0)
+    grads = torch.ops.attnres_hip.packed_backward(flat, q, saved[0], saved[1], upstream.reshape(-1, width),
+                                                  *saved[2:], 1.0)
+    assert torch.equal(out.reshape(-1, width), saved[0]), "out differs from the ops"
+    assert torch.equal(dv.reshape(sources, -1, width), grads[0]), "dv differs from the ops"
+    assert torch.equal(dq, grads[1]), "dq differs from the ops"
+    with torch.no_grad():
+        assert torch.equal(attnres(leaf, query), out.detach()), "the no-grad forward differs"
