@@ -441,3 +441,38 @@ def test_eager_node_random_layouts_match_the_ops(sources, batch, width, rank, la
     assert torch.equal(dq, grads[1]), "dq differs from the ops"
     with torch.no_grad():
         assert torch.equal(attnres(leaf, query), out.detach()), "the no-grad forward differs"
+
+
+@pytest.mark.parametrize("sources,batch,width,rank,layout", _random_layout_cases()[:12])
+def test_eager_list_node_random_layouts_match_the_ops(sources, batch, width, rank, layout):
+    """The same random layouts as a source list (each source a view of the
+    packed tensor, addressable or not): the eager list node against the list
+    ops, bit for bit, and the forward without gradients against the training
+    forward."""
+    torch.manual_seed(sources * 1000 + width + rank + 1)
+    print(f"random list layout S={sources} batch={batch} D={width} R={rank} {layout}", flush=True)
+    if layout == "feature-strided":
+        packed = torch.randn(sources, width, *batch, device="cuda").to(torch.bfloat16)
+        packed = packed.permute(0, *range(2, len(batch) + 2), 1)
+    elif layout == "batch-transposed" and len(batch) >= 2:
+        packed = torch.randn(sources, *batch[::-1], width, device="cuda").to(torch.bfloat16)
+        packed = packed.permute(0, *range(len(batch), 0, -1), len(batch) + 1)
+    else:
+        packed = torch.randn(sources, *batch, width, device="cuda").to(torch.bfloat16)
+    leaves = [packed[s].detach().requires_grad_() for s in range(sources)]
+    query = (torch.randn(rank, device="cuda") / rank ** 0.5).to(torch.bfloat16).requires_grad_()
+    upstream = torch.randn(*batch, width, device="cuda").to(torch.bfloat16)
+    out = attnres(leaves, query)
+    grads = torch.autograd.grad(out, (*leaves, query), upstream)
+
+    from attnres import _ops  # noqa: F401  (registers the ops)
+    listed = [leaf.detach() for leaf in leaves]
+    q = query.detach()
+    saved = torch.ops.attnres_hip.sources_forward(listed, q, 2**-23, 1.0)
+    expected = torch.ops.attnres_hip.sources_backward(listed, q, saved[0], saved[1], upstream, *saved[2:], 1.0)
+    assert torch.equal(out, saved[0]), "out differs from the list ops"
+    for s in range(sources):
+        assert torch.equal(grads[s], expected[s]), f"dv of source {s} differs from the list ops"
+    assert torch.equal(grads[-1], expected[-1]), "dq differs from the list ops"
+    with torch.no_grad():
+        assert torch.equal(attnres(leaves, query), out.detach()), "the no-grad forward differs"
