@@ -17,7 +17,8 @@
   seeded random layouts.
 * Reads without gradients (no_grad, inference_mode, no input requiring
   grad), eager and compiled: the forward alone, no saved state, the training
-  forward's output bit for bit.
+  forward's output bit for bit; checkpointed reads (reentrant or not) against
+  the plain read.
 """
 
 from __future__ import annotations
@@ -476,3 +477,28 @@ def test_eager_list_node_random_layouts_match_the_ops(sources, batch, width, ran
     assert torch.equal(grads[-1], expected[-1]), "dq differs from the list ops"
     with torch.no_grad():
         assert torch.equal(attnres(leaves, query), out.detach()), "the no-grad forward differs"
+
+
+@pytest.mark.parametrize("sources", [5, 9, 25])
+@pytest.mark.parametrize("use_reentrant", [True, False])
+def test_checkpointed_read_matches_the_plain_read(sources, use_reentrant):
+    """torch.utils.checkpoint around a read: the reentrant form runs the first
+    forward under no_grad (the forward alone) and recomputes it with
+    gradients in the backward; both forms give the plain read's output and
+    gradients, bit for bit."""
+    from torch.utils.checkpoint import checkpoint
+
+    torch.manual_seed(17 + sources)
+    print(f"checkpointed read S={sources} reentrant={use_reentrant}", flush=True)
+    values = torch.randn(sources, 2, 150, 2048, device="cuda").to(torch.bfloat16)
+    query = (torch.randn(2048, device="cuda") / 2048 ** 0.5).to(torch.bfloat16)
+    upstream = torch.randn(2, 150, 2048, device="cuda").to(torch.bfloat16)
+
+    def run(wrapped):
+        leaf, q = values.clone().requires_grad_(), query.clone().requires_grad_()
+        out = checkpoint(attnres, leaf, q, use_reentrant=use_reentrant) if wrapped else attnres(leaf, q)
+        out.backward(upstream)
+        return out.detach(), leaf.grad, q.grad
+
+    for name, a, b in zip(("out", "dv", "dq"), run(False), run(True)):
+        assert torch.equal(a, b), f"{name} differs under checkpointing"
