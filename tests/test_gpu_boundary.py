@@ -502,3 +502,31 @@ def test_checkpointed_read_matches_the_plain_read(sources, use_reentrant):
 
     for name, a, b in zip(("out", "dv", "dq"), run(False), run(True)):
         assert torch.equal(a, b), f"{name} differs under checkpointing"
+
+
+@pytest.mark.parametrize("layout", ["packed", "list"])
+@pytest.mark.parametrize("sources", [5, 9, 25])
+def test_frozen_values_give_the_same_query_gradient(layout, sources):
+    """Values that do not require grad (frozen sources) with a trainable
+    query: the node returns no value gradient and the query gradient of the
+    read where both require grad, bit for bit."""
+    torch.manual_seed(23 + sources)
+    print(f"frozen values {layout} S={sources}", flush=True)
+    values = torch.randn(sources, 300, 2048, device="cuda").to(torch.bfloat16)
+    query = (torch.randn(2048, device="cuda") / 2048 ** 0.5).to(torch.bfloat16)
+    upstream = torch.randn(300, 2048, device="cuda").to(torch.bfloat16)
+
+    def read(v, q):
+        return attnres(v if layout == "packed" else list(v.unbind(0)), q)
+
+    both = values.clone().requires_grad_()
+    q_both = query.clone().requires_grad_()
+    out = read(both, q_both)
+    _, dq = torch.autograd.grad(out, (both, q_both), upstream)
+    q_only = query.clone().requires_grad_()
+    frozen = values.clone()
+    out_frozen = read(frozen, q_only)
+    (dq_frozen,) = torch.autograd.grad(out_frozen, (q_only,), upstream)
+    assert torch.equal(out_frozen, out)
+    assert torch.equal(dq_frozen, dq)
+    assert frozen.grad is None
