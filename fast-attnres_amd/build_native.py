@@ -58,6 +58,11 @@ def compile_commands() -> list[tuple[list[str], Path]]:
         units.append((CSRC / "attnres_kernels.hip",
                       [f"-DATTNRES_LANES={lanes}", f"-DATTNRES_CHUNKS={chunks}"],
                       BUILD_DIR / f"attnres_kernels_g{lanes}_c{chunks}.o"))
+    # the (64, 4) token-block backward alone, with LLVM's max-ilp machine scheduler
+    # (1-1.5% faster there, slower for the other kernels; see launch_bwd_block)
+    units.append((CSRC / "attnres_kernels.hip",
+                  ["-DATTNRES_BWD_BLOCK_UNIT", "-mllvm", "-amdgpu-sched-strategy=max-ilp"],
+                  BUILD_DIR / "attnres_kernels_bwd_block.o"))
     return [([hipcc(), f"--offload-arch={ARCH}", *FLAGS, *defines, f"-I{INCLUDE}", f"-I{CSRC}",
               "-c", str(source), "-o", str(obj)], obj)
             for source, defines, obj in units]

@@ -2043,6 +2043,23 @@ int64_t launch_bwd_block(const BwdArgs<Rows, Grads>& a, hipStream_t stream) {
   return blocks;
 }
 
+// The (64, 4) token-block backward is compiled in a translation unit of its
+// own (ATTNRES_BWD_BLOCK_UNIT, end of file) with LLVM's max-ilp machine
+// scheduler; the (64, 4) geometry unit only declares it.  Measured on MI355X
+// (backward alone, us, default scheduler -> max-ilp, two boxes): c2 597.2 /
+// 599.4 / 594.7 / 603.1 -> 589.5 / 586.3 / 587.5 / 593.9; S = 13, N = 32768:
+// 663.3 -> 656.2; S = 49, N = 8192: 568.4 -> 560.7; S = 24: 576.5 -> 572.5;
+// S = 16: 401.5 -> 395.6.  The same scheduler for the whole unit made the
+// forward 3-10% slower and the key-resident backward 0.7% faster; for the
+// (64, 8) unit it was within +-0.6%.  Results are bit-identical: only the
+// instruction order changes.
+#if defined(ATTNRES_LANES) && defined(ATTNRES_CHUNKS) && ATTNRES_LANES == 64 && ATTNRES_CHUNKS == 4
+extern template int64_t launch_bwd_block<64, 4, kBwdBlockTokens, true, PackedRows, PackedGrads>(
+    const BwdArgs<PackedRows, PackedGrads>&, hipStream_t);
+extern template int64_t launch_bwd_block<64, 4, kBwdBlockTokens, true, ListRows, ListGrads>(
+    const BwdArgs<ListRows, ListGrads>&, hipStream_t);
+#endif
+
 template <int G, int CH, bool NOMASK, bool VEC, bool ACC, class Rows, class Grads>
 int64_t launch_bwd(const BwdArgs<Rows, Grads>& a, hipStream_t stream) {
   if constexpr (kBwdBlockVariant<G, CH, NOMASK, VEC, ACC, Grads>) {
@@ -2227,7 +2244,12 @@ void launch_gather_geometry(const GatherArgs& a, bool vec, hipStream_t stream) {
   }
 }
 
-#if defined(ATTNRES_LANES) && defined(ATTNRES_CHUNKS)
+#if defined(ATTNRES_BWD_BLOCK_UNIT)
+template int64_t launch_bwd_block<64, 4, kBwdBlockTokens, true, PackedRows, PackedGrads>(
+    const BwdArgs<PackedRows, PackedGrads>&, hipStream_t);
+template int64_t launch_bwd_block<64, 4, kBwdBlockTokens, true, ListRows, ListGrads>(
+    const BwdArgs<ListRows, ListGrads>&, hipStream_t);
+#elif defined(ATTNRES_LANES) && defined(ATTNRES_CHUNKS)
 template void launch_fwd_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, PackedRows>(const FwdArgs<PackedRows>&, bool,
                                                                              bool, hipStream_t);
 template void launch_fwd_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, ListRows>(const FwdArgs<ListRows>&, bool, bool,
@@ -2250,7 +2272,7 @@ template int64_t launch_bwd_recompute_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, Pa
 template int64_t launch_bwd_recompute_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, ListRows, ListGrads>(
     const BwdArgs<ListRows, ListGrads>&, bool, bool, hipStream_t);
 #else
-#error "compile attnres_kernels.hip with -DATTNRES_LANES=<G> -DATTNRES_CHUNKS=<CH>"
+#error "compile attnres_kernels.hip with -DATTNRES_LANES=<G> -DATTNRES_CHUNKS=<CH>, or -DATTNRES_BWD_BLOCK_UNIT"
 #endif
 
 }  // namespace attnres_hip
