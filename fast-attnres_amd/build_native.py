@@ -8,7 +8,8 @@ library:
 * `csrc/attnres_hip.hip`: the C ABI (`include/attnres_hip.h`), host-side
   argument checks, dispatch and the dq reduction kernels;
 * `csrc/attnres_kernels.hip`, once per row geometry (lanes per token group,
-  16-byte chunks per lane) listed in GEOMETRIES;
+  16-byte chunks per lane) listed in GEOMETRIES, and once more for the
+  (64, 4) token-block backward alone, scheduled with LLVM's max-ilp strategy;
 
 and, against PyTorch's headers and libraries, the eager autograd nodes
 `csrc/attnres_autograd.cpp` -> `attnres/_lib/_autograd.so` (host C++, no
