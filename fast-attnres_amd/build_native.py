@@ -8,8 +8,10 @@ library:
 * `csrc/attnres_hip.hip`: the C ABI (`include/attnres_hip.h`), host-side
   argument checks, dispatch and the dq reduction kernels;
 * `csrc/attnres_kernels.hip`, once per row geometry (lanes per token group,
-  16-byte chunks per lane) listed in GEOMETRIES, and once more for the
-  (64, 4) token-block backward alone, scheduled with LLVM's max-ilp strategy;
+  16-byte chunks per lane) listed in GEOMETRIES, the (64, 8) geometry in two
+  halves (forward, backward) whose backward is scheduled with LLVM's
+  iterative-minreg strategy, and once more for the (64, 4) token-block and
+  whole-row key-resident backwards, scheduled with the max-ilp strategy;
 
 and, against PyTorch's headers and libraries, the eager autograd nodes
 `csrc/attnres_autograd.cpp` -> `attnres/_lib/_autograd.so` (host C++, no
@@ -38,6 +40,13 @@ ARCH = "gfx950"
 # (lanes, chunks) per translation unit; must match ATTNRES_FOR_EACH_GEOMETRY
 # in csrc/attnres_internal.h.
 GEOMETRIES = ((16, 1), (32, 1), (32, 2), (32, 4), (64, 4), (64, 8), (256, 4))
+# geometries built as two units, (forward + gather, backward), with extra flags
+# for the backward half: the (64, 8) backwards (streaming, key-resident,
+# recompute) are 0.4-1.2% faster with the iterative-minreg scheduler, its
+# forwards are not (MI355X, backward us, default -> minreg: S = 16, D = 4096,
+# R = 1024: 777.7 / 786.7 -> 772.7 / 777.5; S = 25, R = D: 1287.9 -> 1282.8;
+# S = 25, R = 1024: 1277.8 -> 1267.3)
+SPLIT_GEOMETRIES = {(64, 8): ["-mllvm", "-amdgpu-sched-strategy=iterative-minreg"]}
 FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 AUTOGRAD_SOURCE = CSRC / "attnres_autograd.cpp"
 AUTOGRAD_OBJECT = BUILD_DIR / "attnres_autograd.o"
@@ -56,14 +65,22 @@ def compile_commands() -> list[tuple[list[str], Path]]:
     """(hipcc command, object path) for every translation unit."""
     units = [(CSRC / "attnres_hip.hip", [], BUILD_DIR / "attnres_hip.o")]
     for lanes, chunks in GEOMETRIES:
-        units.append((CSRC / "attnres_kernels.hip",
-                      [f"-DATTNRES_LANES={lanes}", f"-DATTNRES_CHUNKS={chunks}"],
-                      BUILD_DIR / f"attnres_kernels_g{lanes}_c{chunks}.o"))
-    # the (64, 4) token-block backward alone, with LLVM's max-ilp machine scheduler
-    # (1-1.5% faster there, slower for the other kernels; see launch_bwd_block)
+        defines = [f"-DATTNRES_LANES={lanes}", f"-DATTNRES_CHUNKS={chunks}"]
+        stem = f"attnres_kernels_g{lanes}_c{chunks}"
+        if (lanes, chunks) in SPLIT_GEOMETRIES:
+            units.append((CSRC / "attnres_kernels.hip", [*defines, "-DATTNRES_UNIT_PART=1"],
+                          BUILD_DIR / f"{stem}_fwd.o"))
+            units.append((CSRC / "attnres_kernels.hip",
+                          [*defines, "-DATTNRES_UNIT_PART=2", *SPLIT_GEOMETRIES[(lanes, chunks)]],
+                          BUILD_DIR / f"{stem}_bwd.o"))
+        else:
+            units.append((CSRC / "attnres_kernels.hip", defines, BUILD_DIR / f"{stem}.o"))
+    # the (64, 4) token-block and whole-row key-resident backwards, with LLVM's
+    # max-ilp machine scheduler (1-1.5% faster there, slower for the forwards;
+    # see launch_bwd_block and launch_bwd_keyres_chunks)
     units.append((CSRC / "attnres_kernels.hip",
-                  ["-DATTNRES_BWD_BLOCK_UNIT", "-mllvm", "-amdgpu-sched-strategy=max-ilp"],
-                  BUILD_DIR / "attnres_kernels_bwd_block.o"))
+                  ["-DATTNRES_MAX_ILP_UNIT", "-mllvm", "-amdgpu-sched-strategy=max-ilp"],
+                  BUILD_DIR / "attnres_kernels_max_ilp.o"))
     return [([hipcc(), f"--offload-arch={ARCH}", *FLAGS, *defines, f"-I{INCLUDE}", f"-I{CSRC}",
               "-c", str(source), "-o", str(obj)], obj)
             for source, defines, obj in units]

@@ -2044,15 +2044,14 @@ int64_t launch_bwd_block(const BwdArgs<Rows, Grads>& a, hipStream_t stream) {
 }
 
 // The (64, 4) token-block backward is compiled in a translation unit of its
-// own (ATTNRES_BWD_BLOCK_UNIT, end of file) with LLVM's max-ilp machine
+// own (ATTNRES_MAX_ILP_UNIT, end of file) with LLVM's max-ilp machine
 // scheduler; the (64, 4) geometry unit only declares it.  Measured on MI355X
 // (backward alone, us, default scheduler -> max-ilp, two boxes): c2 597.2 /
 // 599.4 / 594.7 / 603.1 -> 589.5 / 586.3 / 587.5 / 593.9; S = 13, N = 32768:
 // 663.3 -> 656.2; S = 49, N = 8192: 568.4 -> 560.7; S = 24: 576.5 -> 572.5;
 // S = 16: 401.5 -> 395.6.  The same scheduler for the whole unit made the
-// forward 3-10% slower and the key-resident backward 0.7% faster; for the
-// (64, 8) unit it was within +-0.6%.  Results are bit-identical: only the
-// instruction order changes.
+// forward 3-10% slower; for the (64, 8) unit it was within +-0.6%.  Results
+// are bit-identical: only the instruction order changes.
 #if defined(ATTNRES_LANES) && defined(ATTNRES_CHUNKS) && ATTNRES_LANES == 64 && ATTNRES_CHUNKS == 4
 extern template int64_t launch_bwd_block<64, 4, kBwdBlockTokens, true, PackedRows, PackedGrads>(
     const BwdArgs<PackedRows, PackedGrads>&, hipStream_t);
@@ -2154,6 +2153,21 @@ int64_t launch_bwd_keyres_chunks(const BwdArgs<Rows, Grads>& a, hipStream_t stre
   return blocks;
 }
 
+// The whole-row key-resident backward (64 lanes x 4 chunks, D = R = 2048) is
+// compiled in the max-ilp unit too.  Measured on MI355X (c4's shape, S = 9,
+// N = 32768, fwd + bwd loop, backward us, two rounds, default -> max-ilp):
+// 457.3 / 455.4 -> 452.8 / 450.5.
+#if defined(ATTNRES_LANES) && defined(ATTNRES_CHUNKS) && ATTNRES_LANES == 64 && ATTNRES_CHUNKS == 4
+extern template int64_t launch_bwd_keyres_chunks<64, 4, 4, true, PackedRows, PackedGrads>(
+    const BwdArgs<PackedRows, PackedGrads>&, hipStream_t);
+extern template int64_t launch_bwd_keyres_chunks<64, 4, 4, false, PackedRows, PackedGrads>(
+    const BwdArgs<PackedRows, PackedGrads>&, hipStream_t);
+extern template int64_t launch_bwd_keyres_chunks<64, 4, 4, true, ListRows, ListGrads>(
+    const BwdArgs<ListRows, ListGrads>&, hipStream_t);
+extern template int64_t launch_bwd_keyres_chunks<64, 4, 4, false, ListRows, ListGrads>(
+    const BwdArgs<ListRows, ListGrads>&, hipStream_t);
+#endif
+
 template <int G, int CH, class Rows, class Grads>
 int64_t launch_bwd_keyres(const BwdArgs<Rows, Grads>& a, bool vec, hipStream_t stream) {
   if constexpr (G == 64 && CH > kKeyResMaxChunks) {
@@ -2244,16 +2258,33 @@ void launch_gather_geometry(const GatherArgs& a, bool vec, hipStream_t stream) {
   }
 }
 
-#if defined(ATTNRES_BWD_BLOCK_UNIT)
+// Translation units: ATTNRES_MAX_ILP_UNIT holds the (64, 4) kernels built with
+// the max-ilp scheduler; every other unit holds one row geometry
+// (ATTNRES_LANES, ATTNRES_CHUNKS), whole or, with ATTNRES_UNIT_PART, only its
+// forward and gather launchers (1) or only its backward launchers (2), so that
+// the two halves can be built with different scheduler options.
+#if defined(ATTNRES_MAX_ILP_UNIT)
 template int64_t launch_bwd_block<64, 4, kBwdBlockTokens, true, PackedRows, PackedGrads>(
     const BwdArgs<PackedRows, PackedGrads>&, hipStream_t);
 template int64_t launch_bwd_block<64, 4, kBwdBlockTokens, true, ListRows, ListGrads>(
     const BwdArgs<ListRows, ListGrads>&, hipStream_t);
+template int64_t launch_bwd_keyres_chunks<64, 4, 4, true, PackedRows, PackedGrads>(
+    const BwdArgs<PackedRows, PackedGrads>&, hipStream_t);
+template int64_t launch_bwd_keyres_chunks<64, 4, 4, false, PackedRows, PackedGrads>(
+    const BwdArgs<PackedRows, PackedGrads>&, hipStream_t);
+template int64_t launch_bwd_keyres_chunks<64, 4, 4, true, ListRows, ListGrads>(
+    const BwdArgs<ListRows, ListGrads>&, hipStream_t);
+template int64_t launch_bwd_keyres_chunks<64, 4, 4, false, ListRows, ListGrads>(
+    const BwdArgs<ListRows, ListGrads>&, hipStream_t);
 #elif defined(ATTNRES_LANES) && defined(ATTNRES_CHUNKS)
+#if !defined(ATTNRES_UNIT_PART) || ATTNRES_UNIT_PART == 1
 template void launch_fwd_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, PackedRows>(const FwdArgs<PackedRows>&, bool,
                                                                              bool, hipStream_t);
 template void launch_fwd_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, ListRows>(const FwdArgs<ListRows>&, bool, bool,
                                                                            hipStream_t);
+template void launch_gather_geometry<ATTNRES_LANES, ATTNRES_CHUNKS>(const GatherArgs&, bool, hipStream_t);
+#endif
+#if !defined(ATTNRES_UNIT_PART) || ATTNRES_UNIT_PART == 2
 template int64_t launch_bwd_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, PackedRows, PackedGrads>(
     const BwdArgs<PackedRows, PackedGrads>&, bool, bool, bool, hipStream_t);
 template int64_t launch_bwd_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, ListRows, ListGrads>(
@@ -2266,13 +2297,13 @@ template int64_t launch_bwd_geometry_coef<ATTNRES_LANES, ATTNRES_CHUNKS, PackedR
     const BwdArgs<PackedRows, CoefSink>&, bool, bool, hipStream_t);
 template int64_t launch_bwd_geometry_coef<ATTNRES_LANES, ATTNRES_CHUNKS, ListRows>(const BwdArgs<ListRows, CoefSink>&,
                                                                                    bool, bool, hipStream_t);
-template void launch_gather_geometry<ATTNRES_LANES, ATTNRES_CHUNKS>(const GatherArgs&, bool, hipStream_t);
 template int64_t launch_bwd_recompute_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, PackedRows, PackedGrads>(
     const BwdArgs<PackedRows, PackedGrads>&, bool, bool, hipStream_t);
 template int64_t launch_bwd_recompute_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, ListRows, ListGrads>(
     const BwdArgs<ListRows, ListGrads>&, bool, bool, hipStream_t);
+#endif
 #else
-#error "compile attnres_kernels.hip with -DATTNRES_LANES=<G> -DATTNRES_CHUNKS=<CH>, or -DATTNRES_BWD_BLOCK_UNIT"
+#error "compile attnres_kernels.hip with -DATTNRES_LANES=<G> -DATTNRES_CHUNKS=<CH>, or -DATTNRES_MAX_ILP_UNIT"
 #endif
 
 }  // namespace attnres_hip
