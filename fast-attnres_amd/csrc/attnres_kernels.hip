@@ -1824,7 +1824,9 @@ inline int64_t device_cus() {
 // D=1024 two rows are 0.8% slower (occupancy 2 either way), and the
 // accumulating and element-wise variants spill with two.  Rows of 8 chunks
 // (64 lanes, D <= 4096) keep two rows without spilling only unmasked, and
-// are 2-3% slower with them (S=25, N=16384, D=R=4096: 1273 -> 1316).
+// are 2-3% slower with them (S=25, N=16384, D=R=4096: 1273 -> 1316; with the
+// iterative-minreg scheduler of the (64, 8) backward unit too: S=25 1295.5 ->
+// 1329.5, S=13 715.1 -> 727.6, S=48 2487.9 -> 2514.9).
 template <int CH, bool VEC, bool ACC>
 constexpr bool kBwdTwoRowVariant = CH == 4 && VEC && !ACC;
 
