@@ -50,9 +50,10 @@ autocast, entered once per step).  ``model_block`` is the same model on the
 Block schedule; ``model_ref`` is the reference's own 24-layer workload
 (batch 2 x 1024 tokens, vocab 32768, BF16 autocast, fused AdamW).
 
-The c2..c3 lines also carry ``graph_replay``: the forward, the backward and
+The c2..c4 lines also carry ``graph_replay``: the forward, the backward and
 the whole read through the C ABI captured into HIP graphs and replayed (the
-kernels' time without host or launch gaps), median and quartiles over rounds.
+kernels' time without host or launch gaps), median and quartiles over rounds
+(c4: its three reads in each graph, times per read).
 
 ``--copy-probe`` runs only streams of known size (a device copy, and the
 library's partial-sum kernel, whose non-temporal 16-byte accesses match the
@@ -279,6 +280,72 @@ def cpu_baseline(values, query, grad_out, budget_s: float, chunk: int, reads: in
     }
 
 
+def _hip_graph_runtime():
+    """ctypes handles of the HIP runtime torch already loaded, for capturing
+    and replaying graphs of C-ABI calls."""
+    import ctypes
+    import re
+
+    loaded = sorted(set(re.findall(r"\S*libamdhip64\.so\S*", open("/proc/self/maps").read())))
+    hip = ctypes.CDLL(loaded[0])
+    vp, i32 = ctypes.c_void_p, ctypes.c_int
+    for name, args in {"hipStreamBeginCapture": [vp, i32], "hipStreamEndCapture": [vp, ctypes.POINTER(vp)],
+                       "hipGraphInstantiate": [ctypes.POINTER(vp), vp, vp, vp, ctypes.c_size_t],
+                       "hipGraphLaunch": [vp, vp], "hipGraphExecDestroy": [vp], "hipGraphDestroy": [vp]}.items():
+        fn = getattr(hip, name)
+        fn.restype, fn.argtypes = i32, args
+    return hip
+
+
+def _time_graphs(parts: dict, part_bytes: dict, stream, replays: int, rounds: int, reads: int = 1) -> dict:
+    """Capture each part's C-ABI calls into a HIP graph on ``stream`` and
+    replay it ``replays`` times per round over ``rounds`` rounds after one
+    warm-up round; per part the median, quartiles and best round, per read
+    (a part holding ``reads`` reads is divided by it)."""
+    import ctypes
+
+    import torch
+
+    from attnres import _native
+
+    hip = _hip_graph_runtime()
+    vp = ctypes.c_void_p
+    stream.wait_stream(torch.cuda.current_stream())
+    for call in parts["read"]:  # eager first: the library's per-thread launch caches fill outside capture
+        _native.check(call(stream.cuda_stream), "graph-replay read")
+    torch.cuda.synchronize()
+    result = {}
+    for part, calls in parts.items():
+        graph, exe = vp(), vp()
+        assert hip.hipStreamBeginCapture(vp(stream.cuda_stream), 2) == 0  # relaxed
+        for call in calls:
+            _native.check(call(stream.cuda_stream), "graph-replay read")
+        assert hip.hipStreamEndCapture(vp(stream.cuda_stream), ctypes.byref(graph)) == 0
+        assert hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0) == 0
+        try:
+            times = []
+            for round_index in range(rounds + 1):  # round 0 warms up
+                start, stop = _event(), _event()
+                with torch.cuda.stream(stream):
+                    start.record()
+                    for _ in range(replays):
+                        assert hip.hipGraphLaunch(exe, vp(stream.cuda_stream)) == 0
+                    stop.record()
+                torch.cuda.synchronize()
+                if round_index:
+                    times.append(start.elapsed_time(stop) / replays / reads * 1e3)
+        finally:
+            hip.hipGraphExecDestroy(exe)
+            hip.hipGraphDestroy(graph)
+        q1, median, q3 = statistics.quantiles(times, n=4)
+        tbs = part_bytes[part] / (median * 1e-6) / 1e12
+        result[part] = {"us_median": round(median, 2), "us_q1": round(q1, 2), "us_q3": round(q3, 2),
+                        "us_best": round(min(times), 2), "TB/s": round(tbs, 4),
+                        "pct_of_peak": round(100 * tbs / HBM_PEAK_TBS, 2)}
+    result["replays"], result["rounds"] = replays, rounds
+    return result
+
+
 def graph_replay(values, query, grad_out, cfg: dict, replays: int = 20, rounds: int = 11) -> dict:
     """The read through the C ABI, captured into HIP graphs and replayed: the
     reference harness's "cuda_graph" boundary (an event interval around fixed
@@ -286,22 +353,11 @@ def graph_replay(values, query, grad_out, cfg: dict, replays: int = 20, rounds: 
     host or launch gaps.  Three graphs (forward, backward, forward + backward),
     each replayed ``replays`` times per round over ``rounds`` rounds after one
     warm-up round; per graph the median, quartiles and best round."""
-    import ctypes
-    import re
-
     import torch
 
     from attnres import _native
 
     lib = _native.load()
-    loaded = sorted(set(re.findall(r"\S*libamdhip64\.so\S*", open("/proc/self/maps").read())))
-    hip = ctypes.CDLL(loaded[0])  # the runtime torch already loaded
-    vp, i32 = ctypes.c_void_p, ctypes.c_int
-    for name, args in {"hipStreamBeginCapture": [vp, i32], "hipStreamEndCapture": [vp, ctypes.POINTER(vp)],
-                       "hipGraphInstantiate": [ctypes.POINTER(vp), vp, vp, vp, ctypes.c_size_t],
-                       "hipGraphLaunch": [vp, vp], "hipGraphExecDestroy": [vp], "hipGraphDestroy": [vp]}.items():
-        fn = getattr(hip, name)
-        fn.restype, fn.argtypes = i32, args
     S, width, rank = cfg["sources"], cfg["width"], cfg["rank"]
     packed = values.detach().reshape(S, -1, width)
     N = packed.shape[1]
@@ -333,41 +389,72 @@ def graph_replay(values, query, grad_out, cfg: dict, replays: int = 20, rounds: 
     parts = {"forward": (forward,), "backward": (backward,), "read": (forward, backward)}
     fwd_bytes, bwd_bytes = read_bytes(S, N, width)
     part_bytes = {"forward": fwd_bytes, "backward": bwd_bytes, "read": fwd_bytes + bwd_bytes}
-    stream.wait_stream(torch.cuda.current_stream())
-    for call in (forward, backward):  # eager first: the library's per-thread launch caches fill outside capture
-        _native.check(call(stream.cuda_stream), "graph-replay read")
-    torch.cuda.synchronize()
-    result = {}
-    for part, calls in parts.items():
-        graph, exe = vp(), vp()
-        assert hip.hipStreamBeginCapture(vp(stream.cuda_stream), 2) == 0  # relaxed
-        for call in calls:
-            _native.check(call(stream.cuda_stream), "graph-replay read")
-        assert hip.hipStreamEndCapture(vp(stream.cuda_stream), ctypes.byref(graph)) == 0
-        assert hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0) == 0
-        try:
-            times = []
-            for round_index in range(rounds + 1):  # round 0 warms up
-                start, stop = _event(), _event()
-                with torch.cuda.stream(stream):
-                    start.record()
-                    for _ in range(replays):
-                        assert hip.hipGraphLaunch(exe, vp(stream.cuda_stream)) == 0
-                    stop.record()
-                torch.cuda.synchronize()
-                if round_index:
-                    times.append(start.elapsed_time(stop) / replays * 1e3)
-        finally:
-            hip.hipGraphExecDestroy(exe)
-            hip.hipGraphDestroy(graph)
-        q1, median, q3 = statistics.quantiles(times, n=4)
-        tbs = part_bytes[part] / (median * 1e-6) / 1e12
-        result[part] = {"us_median": round(median, 2), "us_q1": round(q1, 2), "us_q3": round(q3, 2),
-                        "us_best": round(min(times), 2), "TB/s": round(tbs, 4),
-                        "pct_of_peak": round(100 * tbs / HBM_PEAK_TBS, 2)}
-    result["replays"], result["rounds"] = replays, rounds
+    result = _time_graphs(parts, part_bytes, stream, replays, rounds)
     result["boundary"] = ("HIP events around back-to-back replays of graphs holding the C-ABI forward, backward, and "
                           "forward + backward (reference harness cuda_graph boundary); TB/s from the median round")
+    return result
+
+
+def graph_replay_list(sources, queries, grad_outs, cfg: dict, replays: int = 20, rounds: int = 11) -> dict:
+    """c4's reads (one ordered source list, one query per read) through the
+    list C ABI, captured into HIP graphs and replayed as graph_replay does for
+    a packed read: graphs of the reads' forwards, their backwards (each into
+    its own gradient rows), and both; times per read."""
+    import ctypes
+
+    import torch
+
+    from attnres import _native
+
+    lib = _native.load()
+    S, width, rank, reads = len(sources), cfg["width"], cfg["rank"], len(queries)
+    N = sources[0].shape[0]
+    dev = sources[0].device
+    rows = [s.detach() for s in sources]
+    if any(r.shape != (N, width) or not r.is_contiguous() for r in rows):
+        raise ValueError("graph_replay_list takes contiguous [N, D] sources")
+    row_ptrs = (ctypes.c_void_p * S)(*[r.data_ptr() for r in rows])
+    strides = (ctypes.c_int64 * S)(*([width] * S))
+    saves = bool(lib.attnres_hip_saves_refinement_for(S, width, rank))
+    ws = torch.empty(lib.attnres_hip_dq_workspace_elems(N, width, rank), device=dev)
+    state = []
+    for k in range(reads):
+        dv = [torch.empty_like(r) for r in rows]
+        state.append({
+            "out": torch.empty(N, width, device=dev, dtype=torch.bfloat16),
+            "refine": torch.empty(N if saves else 0, width, device=dev, dtype=torch.int8),
+            "logit": torch.empty(N, S, device=dev), "inv_rms": torch.empty(N, S, device=dev),
+            "stats": torch.empty(2, N, device=dev), "dv": dv,
+            "dv_ptrs": (ctypes.c_void_p * S)(*[g.data_ptr() for g in dv]),
+            "dq": torch.empty(rank, device=dev, dtype=torch.bfloat16),
+            "query": queries[k].detach(), "grad_out": grad_outs[k].reshape(N, width)})
+    stream = torch.cuda.Stream()
+
+    def forward(k):
+        st = state[k]
+        refine = st["refine"].data_ptr() if saves else None
+        return lambda h: lib.attnres_hip_sources_forward(
+            row_ptrs, strides, S, N, width, st["query"].data_ptr(), rank, 2.0**-23, 1.0, st["out"].data_ptr(),
+            refine, st["logit"].data_ptr(), st["inv_rms"].data_ptr(), st["stats"].data_ptr(), h)
+
+    def backward(k):
+        st = state[k]
+        refine = st["refine"].data_ptr() if saves else None
+        return lambda h: lib.attnres_hip_sources_backward(
+            row_ptrs, strides, S, N, width, st["query"].data_ptr(), rank, 1.0,
+            st["out"].data_ptr() if saves else None, refine, st["grad_out"].data_ptr(), st["logit"].data_ptr(),
+            st["inv_rms"].data_ptr(), st["stats"].data_ptr(), st["dv_ptrs"], st["dq"].data_ptr(), ws.data_ptr(),
+            ws.numel(), h)
+
+    forwards = tuple(forward(k) for k in range(reads))
+    backwards = tuple(backward(k) for k in range(reads))
+    parts = {"forward": forwards, "backward": backwards, "read": forwards + backwards}
+    fwd_bytes, bwd_bytes = read_bytes(S, N, width)
+    part_bytes = {"forward": fwd_bytes, "backward": bwd_bytes, "read": fwd_bytes + bwd_bytes}
+    result = _time_graphs(parts, part_bytes, stream, replays, rounds, reads=reads)
+    result["boundary"] = (f"HIP events around back-to-back replays of graphs holding the {reads} reads' C-ABI list "
+                          "forwards, backwards, and both (reference harness cuda_graph boundary); times per read, "
+                          "TB/s from the median round")
     return result
 
 
@@ -481,6 +568,7 @@ def run_block_schedule(cfg: dict, steps: int, warmup: int, cpu_budget: float | N
         return bank_state["bank"].read(queries[k])
 
     shared_ms = timed(bank_read)
+    graph = graph_replay_list(listed, queries, grad_outs, cfg)
     fwd_bytes, bwd_bytes = read_bytes(cfg["sources"], tokens, width)
     op_ms = fwd_ms + bwd_ms
     value = reads * (fwd_bytes + bwd_bytes) / (op_ms * 1e-3) / 1e12
@@ -504,6 +592,7 @@ def run_block_schedule(cfg: dict, steps: int, warmup: int, cpu_budget: float | N
                        "speedup": round(plain_ms / shared_ms, 3),
                        "what": "forward of the 3 reads + one autograd.grad over them; SharedSources sums "
                                "the source gradients in the backward kernels"},
+        "graph_replay": graph,
         "roofline": {"bound": "hbm", "achieved": round(bwd_tbs * 1e3, 1),
                      "kernel": f"backward op (list layout): {backward_kernel(cfg['sources'], width, rank)} + attnres_dq_reduce_kernel",
                      "peak": HBM_PEAK_TBS * 1e3, "unit": "GB/s", "frac": round(bwd_tbs / HBM_PEAK_TBS, 4),
