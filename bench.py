@@ -630,6 +630,53 @@ def _sweep_one_backward_pass(values, query, grad_out, max_sources: int, steps: i
     return start.elapsed_time(stop) / steps
 
 
+def _sweep_graph_step(values, query, grad_out, max_sources: int, width: int, rank: int,
+                      replays: int = 3, rounds: int = 5) -> dict:
+    """The 48 reads of one (D, R) through the packed C ABI, all captured into
+    one HIP graph (each read's forward, then its backward, in read order) and
+    replayed: the step's kernel time without host or launch gaps, the
+    reference harness's cuda_graph boundary for a whole sweep step.  Read S
+    takes the first S sources of ``values``; the outputs, statistics and
+    gradient rows are buffers sized for S = 48 that every read reuses in
+    turn (stream order keeps each read's forward, backward and the next read
+    apart)."""
+    import torch
+
+    from attnres import _native
+
+    lib = _native.load()
+    N, dev = values.shape[1], values.device
+    out = torch.empty(N, width, device=dev, dtype=torch.bfloat16)
+    refine = torch.empty(N, width, device=dev, dtype=torch.int8)
+    logit, inv_rms = torch.empty(N * max_sources, device=dev), torch.empty(N * max_sources, device=dev)
+    stats = torch.empty(2, N, device=dev)
+    dv = torch.empty_like(values)
+    dq = torch.empty(rank, device=dev, dtype=torch.bfloat16)
+    ws = torch.empty(lib.attnres_hip_dq_workspace_elems(N, width, rank), device=dev)
+    g = grad_out.reshape(N, width)
+    stream = torch.cuda.Stream()
+    calls, step_bytes = [], 0
+    for sources in range(1, max_sources + 1):
+        refine_ptr = refine.data_ptr() if lib.attnres_hip_saves_refinement_for(sources, width, rank) else None
+
+        def forward(h, s=sources, r=refine_ptr):
+            return lib.attnres_hip_packed_forward(values.data_ptr(), N * width, width, s, N, width, query.data_ptr(),
+                                                  rank, 2.0**-23, 1.0, out.data_ptr(), r, logit.data_ptr(),
+                                                  inv_rms.data_ptr(), stats.data_ptr(), h)
+
+        def backward(h, s=sources, r=refine_ptr):
+            return lib.attnres_hip_packed_backward(
+                values.data_ptr(), N * width, width, s, N, width, query.data_ptr(), rank, 1.0,
+                out.data_ptr() if r else None, r, g.data_ptr(), logit.data_ptr(), inv_rms.data_ptr(),
+                stats.data_ptr(), dv.data_ptr(), dq.data_ptr(), ws.data_ptr(), ws.numel(), h)
+
+        calls += [forward, backward]
+        step_bytes += sum(read_bytes(sources, N, width))
+    result = _time_graphs({"read": tuple(calls)}, {"read": step_bytes}, stream, replays, rounds)["read"]
+    return {"ms_per_step": round(result["us_median"] * 1e-3, 4), "ms_q1": round(result["us_q1"] * 1e-3, 4),
+            "ms_q3": round(result["us_q3"] * 1e-3, 4), "TB/s": result["TB/s"], "replays": replays, "rounds": rounds}
+
+
 def backward_kernel(sources: int, width: int, rank: int) -> str:
     """The backward kernel the library launches for a plain read of this shape
     (the save/recompute policy, then the token-block choice for 2048-wide rows)."""
@@ -728,12 +775,14 @@ def run_sweep(cfg: dict, steps: int, warmup: int, cpu_budget: float | None = Non
                 step_ms += ms
                 step_bytes += fwd_bytes + bwd_bytes
             one_pass_ms = _sweep_one_backward_pass(values, query, grad_out, max_sources, steps, warmup)
+            graph_step = _sweep_graph_step(values.detach(), query.detach(), grad_out, max_sources, width, rank)
             del values, grad_out
             torch.cuda.empty_cache()
             sweep.append({"width": width, "rank": rank, "ms_per_step": round(step_ms, 4),
                           "TB/s": round(step_bytes / (step_ms * 1e-3) / 1e12, 4),
                           "one_backward_pass": {"ms_per_step": round(one_pass_ms, 4),
                                                 "TB/s": round(step_bytes / (one_pass_ms * 1e-3) / 1e12, 4)},
+                          "graph_replay": graph_step,
                           "bytes_per_step": step_bytes, "per_read_S_us_TBs": per_read})
             total_bytes += step_bytes
             total_ms += step_ms
@@ -748,7 +797,8 @@ def run_sweep(cfg: dict, steps: int, warmup: int, cpu_budget: float | None = Non
         "config": {"workload": cfg["name"], "tokens": tokens, "layout": "packed",
                    "note": "ms_per_step is the mean over the four (D, R) steps; each step's own time is in sweep "
                            "(reads timed one by one, one autograd.grad call each); one_backward_pass: the same "
-                           "48 reads with all forwards, then one autograd.backward"},
+                           "48 reads with all forwards, then one autograd.backward; graph_replay: the 48 reads' "
+                           "C-ABI forwards and backwards captured into one HIP graph and replayed (median round)"},
         "one_backward_pass": {"ms_per_step": round(sum(x["one_backward_pass"]["ms_per_step"] for x in sweep)
                                                    / len(sweep), 4),
                               "TB/s": round(total_bytes / (sum(x["one_backward_pass"]["ms_per_step"] for x in sweep)

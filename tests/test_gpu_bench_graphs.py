@@ -1,6 +1,8 @@
 """bench.py's graph-replay boundary (the C-ABI read captured into HIP graphs
-and replayed) on small cases: the packed form the c2/c3 lines use and the
-list form of the c4 line (three reads of one source list, one query each).
+and replayed) on small cases: the packed form the c2/c3 lines use, the
+list form of the c4 line (three reads of one source list, one query each)
+and the whole-step graph of the c5 sweep (the reads of S = 1..n in one
+graph).
 The replayed calls must succeed and every part must carry ordered
 quartiles; the numerics of captured reads are covered by test_gpu_graphs.
 """
@@ -55,3 +57,18 @@ def test_graph_replay_packed_times_every_part():
     record = bench.graph_replay(values, query, grad_out, {"sources": 6, "width": 2048, "rank": 512},
                                 replays=3, rounds=3)
     _check(record)
+
+
+@pytest.mark.parametrize("width,rank", [(1024, 256), (2048, 2048)])
+def test_sweep_graph_step_replays_every_read(width, rank):
+    """c5's whole-step graph: the reads of S = 1..14 (recompute, key-resident,
+    saved-path and, at 2048, token-block backwards) in one captured graph."""
+    print(f"sweep graph step S=1..14 N=200 D={width} R={rank}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(2)
+    dev = torch.device("cuda:0")
+    values = torch.randn(14, 200, width, device=dev, generator=g).to(torch.bfloat16)
+    query = (torch.randn(rank, device=dev, generator=g) / rank**0.5).to(torch.bfloat16)
+    grad_out = torch.randn(200, width, device=dev, generator=g).to(torch.bfloat16)
+    record = bench._sweep_graph_step(values, query, grad_out, 14, width, rank, replays=2, rounds=3)
+    assert 0 < record["ms_q1"] <= record["ms_per_step"] <= record["ms_q3"], record
+    assert record["TB/s"] > 0
