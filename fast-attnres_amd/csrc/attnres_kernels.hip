@@ -1946,7 +1946,9 @@ constexpr bool kFwdBlockWideVariant = G == kBlock && CH == 4 && VEC;
 // 640, R = 160: S = 25: 115.1 -> 101.5; but S = 5: 37.2 -> 38.9 (D = 768);
 // D = 256 (1 chunk): S = 9: 24.8 -> 23.4, S = 25: 51.2 -> 45.8; D = 200: S =
 // 48: 86.6 -> 79.8.  Full rows of 1024 were within +-3% either way and keep
-// the one-token kernel, as do 16-lane groups (D <= 128: within +-1.5%) and
+// the one-token kernel (a wavefront per token instead, 64 lanes of 2 chunks,
+// four or eight tokens, was slower: S = 25, N = 16384, R = D: 153 -> 165-172,
+// S = 48: 282-290 -> 292-309; S = 13 equal), as do 16-lane groups (D <= 128: within +-1.5%) and
 // rows that are not 16-byte aligned (D = 3000, 1000, 5000: within +-1%).
 template <int G, int CH, bool VEC>
 constexpr bool kFwdBlock32NarrowVariant = G == 32 && CH <= 2 && VEC;
