@@ -9,9 +9,10 @@ library:
   argument checks, dispatch and the dq reduction kernels;
 * `csrc/attnres_kernels.hip`, once per row geometry (lanes per token group,
   16-byte chunks per lane) listed in GEOMETRIES, the (64, 8) geometry in two
-  halves (forward, backward) whose backward is scheduled with LLVM's
-  iterative-minreg strategy, and once more for the (64, 4) token-block and
-  whole-row key-resident backwards, scheduled with the max-ilp strategy;
+  parts (1: unmasked forwards and gather; 2: backwards and masked forwards)
+  whose part 2 is scheduled with LLVM's iterative-minreg strategy, and once
+  more for the (64, 4) token-block and whole-row key-resident backwards,
+  scheduled with the max-ilp strategy;
 
 and, against PyTorch's headers and libraries, the eager autograd nodes
 `csrc/attnres_autograd.cpp` -> `attnres/_lib/_autograd.so` (host C++, no
@@ -40,12 +41,14 @@ ARCH = "gfx950"
 # (lanes, chunks) per translation unit; must match ATTNRES_FOR_EACH_GEOMETRY
 # in csrc/attnres_internal.h.
 GEOMETRIES = ((16, 1), (32, 1), (32, 2), (32, 4), (64, 4), (64, 8), (256, 4))
-# geometries built as two units, (forward + gather, backward), with extra flags
-# for the backward half: the (64, 8) backwards (streaming, key-resident,
-# recompute) are 0.4-1.2% faster with the iterative-minreg scheduler, its
-# forwards are not (MI355X, backward us, default -> minreg: S = 16, D = 4096,
-# R = 1024: 777.7 / 786.7 -> 772.7 / 777.5; S = 25, R = D: 1287.9 -> 1282.8;
-# S = 25, R = 1024: 1277.8 -> 1267.3)
+# geometries built as two units (ATTNRES_UNIT_PART 1: forwards and gather;
+# 2: backwards, and for (64, 8) the masked forwards), with extra flags for
+# part 2: the (64, 8) backwards (streaming, key-resident, recompute) are
+# 0.4-1.2% faster with the iterative-minreg scheduler and its masked forwards
+# 1-2%, its unmasked forwards are not (MI355X, backward us, default -> minreg:
+# S = 16, D = 4096, R = 1024: 777.7 / 786.7 -> 772.7 / 777.5; S = 25, R = D:
+# 1287.9 -> 1282.8; S = 25, R = 1024: 1277.8 -> 1267.3; forwards: see
+# launch_fwd)
 SPLIT_GEOMETRIES = {(64, 8): ["-mllvm", "-amdgpu-sched-strategy=iterative-minreg"]}
 FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 AUTOGRAD_SOURCE = CSRC / "attnres_autograd.cpp"
@@ -69,10 +72,10 @@ def compile_commands() -> list[tuple[list[str], Path]]:
         stem = f"attnres_kernels_g{lanes}_c{chunks}"
         if (lanes, chunks) in SPLIT_GEOMETRIES:
             units.append((CSRC / "attnres_kernels.hip", [*defines, "-DATTNRES_UNIT_PART=1"],
-                          BUILD_DIR / f"{stem}_fwd.o"))
+                          BUILD_DIR / f"{stem}_part1.o"))
             units.append((CSRC / "attnres_kernels.hip",
                           [*defines, "-DATTNRES_UNIT_PART=2", *SPLIT_GEOMETRIES[(lanes, chunks)]],
-                          BUILD_DIR / f"{stem}_bwd.o"))
+                          BUILD_DIR / f"{stem}_part2.o"))
         else:
             units.append((CSRC / "attnres_kernels.hip", defines, BUILD_DIR / f"{stem}.o"))
     # the (64, 4) token-block and whole-row key-resident backwards, with LLVM's

@@ -1992,6 +1992,23 @@ void launch_fwd(const FwdArgs<Rows>& a, hipStream_t stream) {
                      dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream, a);
 }
 
+// The masked forwards of the (64, 8) geometry (2048 < D <= 4096, R < D) are
+// compiled with that geometry's backward launchers (ATTNRES_UNIT_PART 2, the
+// iterative-minreg machine scheduler); part 1 only declares them.  Measured on
+// MI355X (forward alone, N = 16384, R = 1024, us, three rounds, default ->
+// minreg): S = 16 381.1 / 390.5 / 377.3 -> 371.0 / 385.9 / 368.9; S = 13
+// 309.1 / 307.8 / 308.2 -> 305.8 / 304.6 / 306.0; S = 25 566.6 / 568.8 /
+// 571.0 -> 556.5 / 561.2 / 564.3; S = 48 1044.7 / 1039.0 / 1047.6 -> 1024.3 /
+// 1026.9 / 1023.5.  The unmasked ones (R = D) were slower with it (S = 16:
+// 388.5 / 392.0 / 386.2 -> 400.1 / 395.7 / 396.2) and stay in part 1.
+#if defined(ATTNRES_LANES) && defined(ATTNRES_CHUNKS) && ATTNRES_LANES == 64 && ATTNRES_CHUNKS == 8 && \
+    defined(ATTNRES_UNIT_PART) && ATTNRES_UNIT_PART == 1
+extern template void launch_fwd<64, 8, false, true, PackedRows>(const FwdArgs<PackedRows>&, hipStream_t);
+extern template void launch_fwd<64, 8, false, false, PackedRows>(const FwdArgs<PackedRows>&, hipStream_t);
+extern template void launch_fwd<64, 8, false, true, ListRows>(const FwdArgs<ListRows>&, hipStream_t);
+extern template void launch_fwd<64, 8, false, false, ListRows>(const FwdArgs<ListRows>&, hipStream_t);
+#endif
+
 template <int G, int CH, class Rows>
 void launch_fwd_geometry(const FwdArgs<Rows>& a, bool nomask, bool vec, hipStream_t stream) {
   if (nomask) {
@@ -2265,8 +2282,9 @@ void launch_gather_geometry(const GatherArgs& a, bool vec, hipStream_t stream) {
 // Translation units: ATTNRES_MAX_ILP_UNIT holds the (64, 4) kernels built with
 // the max-ilp scheduler; every other unit holds one row geometry
 // (ATTNRES_LANES, ATTNRES_CHUNKS), whole or, with ATTNRES_UNIT_PART, only its
-// forward and gather launchers (1) or only its backward launchers (2), so that
-// the two halves can be built with different scheduler options.
+// forward and gather launchers (1) or only its backward launchers (2; for the
+// (64, 8) geometry also its masked forwards, see launch_fwd), so that the two
+// parts can be built with different scheduler options.
 #if defined(ATTNRES_MAX_ILP_UNIT)
 template int64_t launch_bwd_block<64, 4, kBwdBlockTokens, true, PackedRows, PackedGrads>(
     const BwdArgs<PackedRows, PackedGrads>&, hipStream_t);
@@ -2287,6 +2305,12 @@ template void launch_fwd_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, PackedRows>(con
 template void launch_fwd_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, ListRows>(const FwdArgs<ListRows>&, bool, bool,
                                                                            hipStream_t);
 template void launch_gather_geometry<ATTNRES_LANES, ATTNRES_CHUNKS>(const GatherArgs&, bool, hipStream_t);
+#endif
+#if defined(ATTNRES_UNIT_PART) && ATTNRES_UNIT_PART == 2 && ATTNRES_LANES == 64 && ATTNRES_CHUNKS == 8
+template void launch_fwd<64, 8, false, true, PackedRows>(const FwdArgs<PackedRows>&, hipStream_t);
+template void launch_fwd<64, 8, false, false, PackedRows>(const FwdArgs<PackedRows>&, hipStream_t);
+template void launch_fwd<64, 8, false, true, ListRows>(const FwdArgs<ListRows>&, hipStream_t);
+template void launch_fwd<64, 8, false, false, ListRows>(const FwdArgs<ListRows>&, hipStream_t);
 #endif
 #if !defined(ATTNRES_UNIT_PART) || ATTNRES_UNIT_PART == 2
 template int64_t launch_bwd_geometry<ATTNRES_LANES, ATTNRES_CHUNKS, PackedRows, PackedGrads>(

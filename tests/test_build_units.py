@@ -1,7 +1,8 @@
 """The library's translation units (fast-attnres_amd/build_native.py), on the
 CPU: every row geometry of the dispatch table is compiled for gfx950 with the
-packed-FP32 VALU ops disabled; the 4096-wide geometry is built as a forward
-half (default scheduler) and a backward half (iterative-minreg); one more unit
+packed-FP32 VALU ops disabled; the 4096-wide geometry is built in two parts,
+its unmasked forwards and gather (default scheduler) and its backwards and
+masked forwards (iterative-minreg); one more unit
 holds the 2048-wide token-block and whole-row key-resident backwards built
 with the max-ilp scheduler.  A unit dropped from the list would leave
 launchers undefined in the shared library, which the loader reports only on
@@ -52,7 +53,7 @@ def test_every_geometry_has_its_units():
         defines = [f"-DATTNRES_LANES={lanes}", f"-DATTNRES_CHUNKS={chunks}"]
         if (lanes, chunks) in build_native.SPLIT_GEOMETRIES:
             assert f"{stem}.o" not in units
-            forward, backward = units[f"{stem}_fwd.o"], units[f"{stem}_bwd.o"]
+            forward, backward = units[f"{stem}_part1.o"], units[f"{stem}_part2.o"]
             assert all(d in forward for d in defines) and "-DATTNRES_UNIT_PART=1" in forward
             assert all(d in backward for d in defines) and "-DATTNRES_UNIT_PART=2" in backward
             assert not any(a.startswith("-amdgpu-sched-strategy") for a in forward)
@@ -86,5 +87,30 @@ def test_built_library_leaves_no_attnres_symbol_undefined():
     defined = subprocess.run([nm, "-C", "--defined-only", str(lib)], capture_output=True, text=True,
                              check=True).stdout
     for launcher in ("launch_bwd_block<64, 4, 4, true", "launch_bwd_keyres_chunks<64, 4, 4, true",
-                     "launch_bwd_geometry<64, 8", "launch_fwd_geometry<64, 8"):
+                     "launch_bwd_geometry<64, 8", "launch_fwd_geometry<64, 8",
+                     "launch_fwd<64, 8, false, true"):
         assert launcher in defined, launcher
+
+
+def test_scheduler_units_hold_the_only_definitions():
+    """Template instances are weak symbols: if a default-scheduler unit also
+    instantiated a launcher that a scheduler unit provides, the linker would
+    keep either copy without a word.  The default units must only reference
+    them (nm 'U'), the scheduler units define them."""
+    nm = shutil.which("nm")
+    build = build_native.BUILD_DIR
+    pairs = {
+        "attnres_kernels_g64_c8_part1.o": ("attnres_kernels_g64_c8_part2.o", "launch_fwd<64, 8, false, "),
+        "attnres_kernels_g64_c4.o": ("attnres_kernels_max_ilp.o", "launch_bwd_block<64, 4, 4, true, "),
+    }
+    if nm is None or not all((build / a).exists() and (build / b).exists() for a, (b, _) in pairs.items()):
+        pytest.skip("objects not built or nm missing")
+
+    def symbol_lines(obj, needle):
+        out = subprocess.run([nm, "-C", str(build / obj)], capture_output=True, text=True, check=True).stdout
+        return [line for line in out.splitlines() if needle in line]
+
+    for plain, (scheduled, needle) in pairs.items():
+        plain_lines, scheduled_lines = symbol_lines(plain, needle), symbol_lines(scheduled, needle)
+        assert plain_lines and all(line.split()[0] == "U" for line in plain_lines), plain
+        assert scheduled_lines and all(line.split()[1] in ("W", "T") for line in scheduled_lines), scheduled
