@@ -2071,8 +2071,11 @@ int64_t launch_bwd_block(const BwdArgs<Rows, Grads>& a, hipStream_t stream) {
 // 599.4 / 594.7 / 603.1 -> 589.5 / 586.3 / 587.5 / 593.9; S = 13, N = 32768:
 // 663.3 -> 656.2; S = 49, N = 8192: 568.4 -> 560.7; S = 24: 576.5 -> 572.5;
 // S = 16: 401.5 -> 395.6.  The same scheduler for the whole unit made the
-// forward 3-10% slower; for the (64, 8) unit it was within +-0.6%.  Results
-// are bit-identical: only the instruction order changes.
+// forward 3-10% slower; for the (64, 8) unit it was within +-0.6%.  LLVM's
+// iterative-minreg strategy made this kernel slower (three rounds, us, max-ilp
+// -> minreg: c2 583.7-592.0 -> 604.0-613.0; S = 13, N = 32768 646.6-653.4 ->
+// 665.2-671.6; S = 49, N = 8192 558.0-562.5 -> 578.1-581.6).  Results are
+// bit-identical: only the instruction order changes.
 #if defined(ATTNRES_LANES) && defined(ATTNRES_CHUNKS) && ATTNRES_LANES == 64 && ATTNRES_CHUNKS == 4
 extern template int64_t launch_bwd_block<64, 4, kBwdBlockTokens, true, PackedRows, PackedGrads>(
     const BwdArgs<PackedRows, PackedGrads>&, hipStream_t);
